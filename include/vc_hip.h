@@ -1,0 +1,187 @@
+/*
+ * vc_hip.h — C ABI of the MI355X (gfx950) backend for VectorCore.
+ *
+ * This is the drop-in device boundary: every entry point replaces one member
+ * of the reference's device interface `MetalBackend`
+ * (include/vectorcore/metal_backend.hpp:13-63, implemented in
+ * src/metal/metal_backend.mm), or is a fused backward kernel that a backward
+ * rule in src/ops.cpp / src/nn.cpp calls instead of a chain of those members.
+ *
+ * Conventions
+ *  - Plain C: device buffers are `float*` (or `void*`) device addresses, sizes
+ *    are element counts unless the name says bytes. No C++ or torch types.
+ *  - Every function returns a status (VC_HIP_OK == 0). On failure,
+ *    vc_hip_last_error() holds a message for the calling thread. The ABI never
+ *    throws; the C++ wrapper maps statuses to the reference's exception types
+ *    (invalid_argument, out_of_range, overflow_error, runtime_error).
+ *  - Work is enqueued on one in-order HIP stream owned by the library and runs
+ *    asynchronously. Only vc_hip_download() and vc_hip_synchronize() wait for
+ *    the device; asynchronous device faults are reported by those two calls.
+ *  - Output buffers are allocated by the caller (vc_hip_alloc) and fully
+ *    written by the kernel. The library never frees memory it did not
+ *    allocate.
+ */
+#ifndef VC_HIP_H
+#define VC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------- */
+#define VC_HIP_OK 0
+#define VC_HIP_ERR_INVALID_ARGUMENT 1 /* std::invalid_argument in the reference */
+#define VC_HIP_ERR_OUT_OF_RANGE 2     /* std::out_of_range */
+#define VC_HIP_ERR_OVERFLOW 3         /* std::overflow_error */
+#define VC_HIP_ERR_RUNTIME 4          /* std::runtime_error (HIP failure, device fault) */
+#define VC_HIP_ERR_UNAVAILABLE 5      /* no usable gfx950 device */
+#define VC_HIP_ERR_OUT_OF_MEMORY 6
+
+/* ---- operation codes: same order as the reference enums
+ *      (include/vectorcore/cpu_backend.hpp:9-11) ------------------------- */
+#define VC_BINARY_ADD 0
+#define VC_BINARY_SUBTRACT 1
+#define VC_BINARY_MULTIPLY 2
+#define VC_BINARY_DIVIDE 3
+#define VC_UNARY_NEGATE 0
+#define VC_UNARY_RELU 1
+#define VC_UNARY_SIGMOID 2
+#define VC_UNARY_RELU_GRADIENT 3
+#define VC_UNARY_EXP 4
+#define VC_UNARY_LOG 5
+#define VC_REDUCE_SUM 0
+#define VC_REDUCE_MAX 1
+#define VC_REDUCE_ARGMAX 2
+
+/* ---- device and errors --------------------------------------------------- */
+/* MetalBackend::available (metal_backend.hpp:18). Initialises on first call. */
+int vc_hip_available(void);
+/* MetalBackend::device_name (metal_backend.hpp:19). */
+const char* vc_hip_device_name(void);
+/* MetalBackend::last_error (metal_backend.hpp:20): thread-local message of
+ * the last failing call on this thread, or why the device is unavailable. */
+const char* vc_hip_last_error(void);
+/* MetalBackend::gemm_kernel (metal_backend.hpp:22): "mfma" (MFMA tiles),
+ * "simple" (portable FMA tiles, forced by VECTORCORE_HIP_GEMM=simple),
+ * or "unavailable". */
+const char* vc_hip_gemm_kernel(void);
+
+/* ---- memory (stream-ordered size-class pool) ----------------------------- */
+/* MetalBackend::allocate (metal_backend.hpp:23, metal_backend.mm:161-182). */
+int vc_hip_alloc(size_t bytes, void** out);
+/* The Metal storage destructor's release (metal_backend.mm:35, 188-191): the
+ * buffer returns to the pool at once; stream order keeps queued users safe. */
+int vc_hip_release(void* buffer);
+/* MetalBackend::upload (metal_backend.hpp:24): copies `bytes` from host
+ * memory; returns once the host memory may be reused (staged, no device wait). */
+int vc_hip_upload(void* dst, const void* src, size_t bytes);
+/* MetalBackend::download (metal_backend.hpp:26): waits for queued work. */
+int vc_hip_download(void* dst, const void* src, size_t bytes);
+/* Device-to-device copy on the library stream. */
+int vc_hip_copy(void* dst, const void* src, size_t bytes);
+/* MetalBackend::synchronize (metal_backend.hpp:55): waits and reports any
+ * asynchronous device error. */
+int vc_hip_synchronize(void);
+
+typedef struct vc_hip_pool_stats {
+    uint64_t device_allocations; /* hipMalloc calls made by the pool */
+    uint64_t reuses;             /* allocations served from the free lists */
+    uint64_t live_bytes;         /* bytes handed out and not yet released */
+    uint64_t pooled_bytes;       /* bytes parked in the free lists */
+} vc_hip_pool_stats;
+int vc_hip_pool_stats_get(vc_hip_pool_stats* out);
+/* Returns every parked buffer to the device (waits for queued work). */
+int vc_hip_pool_trim(void);
+
+/* ---- elementwise ----------------------------------------------------------- */
+int vc_hip_fill(float* out, size_t count, float value);
+/* MetalBackend::binary (metal_backend.hpp:28-31): out[i] = a[.] op b[.] with
+ * broadcasting by shape/strides (rank <= 8). */
+int vc_hip_binary(const float* a, const size_t* a_shape, const size_t* a_strides, size_t a_rank,
+                  const float* b, const size_t* b_shape, const size_t* b_strides, size_t b_rank,
+                  float* out, const size_t* out_shape, size_t out_rank, int op);
+/* Binary op with one operand a host-side scalar value (the scalar tensors of
+ * src/tensor.cpp:323-330), so no device scalar has to be read:
+ * out = a op s (scalar_first == 0) or s op a (scalar_first != 0). */
+int vc_hip_binary_scalar(const float* a, size_t count, float s, int scalar_first, float* out, int op);
+/* MetalBackend::unary (metal_backend.hpp:32-33). */
+int vc_hip_unary(const float* in, float* out, size_t count, int op);
+/* MetalBackend::axpy_inplace (metal_backend.hpp:53-54): target += alpha * source. */
+int vc_hip_axpy(float* target, const float* source, size_t count, float alpha);
+
+/* Fused activation gradients (one pass each; same-shape contiguous operands).
+ * relu:    out = grad * (input > 0 ? 1 : 0)         (src/ops.cpp:398-401)
+ * sigmoid: out = (grad * y) * (1 - y), y the output  (src/ops.cpp:408-411)
+ * exp:     out = grad * y, y the output              (src/ops.cpp:363-365)
+ * log:     out = grad / input                        (src/ops.cpp:372-374) */
+int vc_hip_relu_backward(const float* grad, const float* input, float* out, size_t count);
+int vc_hip_sigmoid_backward(const float* grad, const float* output, float* out, size_t count);
+int vc_hip_exp_backward(const float* grad, const float* output, float* out, size_t count);
+int vc_hip_log_backward(const float* grad, const float* input, float* out, size_t count);
+/* Division gradient before sum_to_shape (src/ops.cpp:148-154), over the
+ * output shape with a and b broadcast: grad_a = grad / b,
+ * grad_b = -(grad * a) / (b * b). Either output may be NULL. */
+int vc_hip_div_backward(const float* grad, const float* a, const size_t* a_shape, const size_t* a_strides,
+                        size_t a_rank, const float* b, const size_t* b_shape, const size_t* b_strides,
+                        size_t b_rank, const size_t* out_shape, size_t out_rank, float* grad_a, float* grad_b);
+
+/* ---- matrix multiply ------------------------------------------------------- */
+/* MetalBackend::matmul (metal_backend.hpp:34-40): for z < batch,
+ * c[z*m*n ...] = op(a + a_offsets[z]) @ op(b + b_offsets[z]); op transposes
+ * when trans_* is set (a stored k x m, b stored n x k), read in place. */
+int vc_hip_matmul(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                  const size_t* a_offsets, const size_t* b_offsets, size_t batch, int trans_a, int trans_b);
+/* Batch-reduced product for gradients of a batch-broadcast operand
+ * (src/ops.cpp:252-260 followed by sum_to_shape over the batch):
+ * c = sum_{z < count} op(a + z*a_stride) @ op(b + z*b_stride), one fixed order. */
+int vc_hip_matmul_reduce(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                         size_t count, size_t a_stride, size_t b_stride, int trans_a, int trans_b);
+/* MetalBackend::transpose_last2 (metal_backend.hpp:42-43). */
+int vc_hip_transpose_last2(const float* in, float* out, size_t batch, size_t rows, size_t cols);
+
+/* ---- reductions -------------------------------------------------------------- */
+/* MetalBackend::reduce_sum (metal_backend.hpp:44-45): out[0] = sum(in),
+ * accumulated in double over a shape-fixed partition (deterministic). */
+int vc_hip_reduce_sum(const float* in, size_t count, float* out);
+/* MetalBackend::reduce_axis (metal_backend.hpp:46-48): [outer, length, inner]
+ * -> [outer, inner]. Sum accumulates in double in a shape-fixed order; max and
+ * argmax return the first maximum (argmax as a float index), and a NaN first
+ * element wins, as in src/cpu/cpu_backend.cpp:443-457. */
+int vc_hip_reduce_axis(const float* in, float* out, size_t outer, size_t length, size_t inner, int op);
+/* MetalBackend::scatter_axis (metal_backend.hpp:49-51). */
+int vc_hip_scatter_axis(const float* values, const float* indices, float* out, size_t outer, size_t length,
+                        size_t inner);
+
+/* ---- softmax cross-entropy (fused loss node for src/nn.cpp:31-53) ------------- */
+/* loss[0] = -(sum_i log_softmax(logits)_i[targets_i]) / rows, with the
+ * reference's composition order; row_stats[2*i] = row max, row_stats[2*i+1] =
+ * sum_j exp(x_ij - max) (saved for the backward). targets are class indices
+ * already checked against `classes` by the caller. */
+int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows, size_t classes,
+                        float* row_stats, float* loss);
+/* grad_logits = (softmax(logits) - onehot(targets)) * grad_loss[0] / rows,
+ * evaluated as the reference's composed backward does. grad_loss is a device
+ * scalar (the upstream gradient of the loss). */
+int vc_hip_xent_backward(const float* logits, const int32_t* targets, const float* row_stats,
+                         const float* grad_loss, size_t rows, size_t classes, float* grad_logits);
+
+/* ---- measurement ------------------------------------------------------------- */
+/* When enabled, each kernel launch is bracketed by HIP events on the library
+ * stream and its algorithmic work (FLOPs, bytes) is recorded by label. */
+int vc_hip_profile_enable(int enable);
+int vc_hip_profile_reset(void);
+/* Waits for the stream, then reports the number of distinct labels. */
+int vc_hip_profile_count(size_t* labels);
+/* Aggregate of label i: launches, summed device time (ms), summed FLOPs and
+ * algorithmic HBM bytes. The label string stays valid until the next reset. */
+int vc_hip_profile_entry(size_t i, const char** label, uint64_t* launches, double* milliseconds,
+                         double* flops, double* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VC_HIP_H */

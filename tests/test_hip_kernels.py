@@ -1,0 +1,305 @@
+"""GPU parity of every C-ABI entry point (include/vc_hip.h) against the oracle.
+
+Bars: bit-exact for indices (argmax), for pure-fp32 elementwise chains and
+for data movement; the reference's own tolerance pairs elsewhere (GEMM:
+rtol 1e-4, atol 1e-4 sqrt(k), tests/python/test_performance_paths.py:43;
+reductions rtol 1e-4 and BASELINE's 1e-4 relative; transcendental
+elementwise results within 1e-5 relative, BASELINE's elementwise bar).
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import kernels as K
+from tests.golden.make_golden import GEMM_SHAPES, gemm_inputs
+from vectorcore_amd import cabi as C
+from vectorcore_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    assert C.available(), C.lib().vc_hip_last_error().decode()
+    yield
+    C.synchronize()
+
+
+def run_gemm(a, b, m, k, n, ta, tb, batch=1, a_offsets=None, b_offsets=None):
+    da, db = C.Buffer.of(a), C.Buffer.of(b)
+    dc = C.Buffer((batch, m, n))
+    ao = a_offsets if a_offsets is not None else [z * m * k for z in range(batch)]
+    bo = b_offsets if b_offsets is not None else [z * k * n for z in range(batch)]
+    C.check(C.lib().vc_hip_matmul(da.ptr, db.ptr, dc.ptr, m, k, n, C.sizes(ao), C.sizes(bo), batch, int(ta), int(tb)))
+    return dc.numpy()
+
+
+@pytest.mark.parametrize("m,k,n", GEMM_SHAPES)
+def test_gemm_matches_reference_fixture(golden, m, k, n):
+    for ta in (0, 1):
+        for tb in (0, 1):
+            a, b = gemm_inputs(m, k, n, ta, tb)
+            got = run_gemm(a, b, m, k, n, ta, tb)[0]
+            np.testing.assert_allclose(got, golden[f"gemm_{m}_{k}_{n}_{ta}{tb}_c"], rtol=1e-4, atol=1e-4 * np.sqrt(k),
+                                       err_msg=f"trans_a={ta} trans_b={tb}")
+
+
+@pytest.mark.parametrize("m,k,n", [(128, 64, 128), (192, 256, 64), (128, 60, 128), (130, 64, 128), (128, 64, 70),
+                                   (257, 129, 383), (512, 1024, 1000), (1, 4096, 3), (1000, 7, 1)])
+def test_gemm_edges_against_oracle(m, k, n):
+    rng = np.random.default_rng(m * 7 + k * 3 + n)
+    for ta in (0, 1):
+        for tb in (0, 1):
+            a = rng.uniform(-1, 1, size=(k, m) if ta else (m, k)).astype(np.float32)
+            b = rng.uniform(-1, 1, size=(n, k) if tb else (k, n)).astype(np.float32)
+            np.testing.assert_allclose(run_gemm(a, b, m, k, n, ta, tb)[0], K.matmul2d(a, b, bool(ta), bool(tb)),
+                                       rtol=1e-4, atol=1e-4 * np.sqrt(k), err_msg=f"trans_a={ta} trans_b={tb}")
+
+
+def test_gemm_batched_offsets_affine_and_table():
+    rng = np.random.default_rng(3)
+    m, k, n = 33, 70, 41
+    a = rng.standard_normal((4, m, k)).astype(np.float32)
+    b = rng.standard_normal((2, k, n)).astype(np.float32)
+    # batch z reads a[z] and b[z % 2]: not affine, goes through the offset table
+    got = run_gemm(a, b, m, k, n, 0, 0, batch=4, a_offsets=[z * m * k for z in range(4)],
+                   b_offsets=[(z % 2) * k * n for z in range(4)])
+    for z in range(4):
+        np.testing.assert_allclose(got[z], K.matmul2d(a[z], b[z % 2]), rtol=1e-4, atol=1e-4 * np.sqrt(k))
+    # broadcast B: affine with stride 0
+    got = run_gemm(a, b, m, k, n, 0, 0, batch=4, b_offsets=[0, 0, 0, 0])
+    for z in range(4):
+        np.testing.assert_allclose(got[z], K.matmul2d(a[z], b[0]), rtol=1e-4, atol=1e-4 * np.sqrt(k))
+
+
+def test_gemm_batch_reduce_matches_summed_products():
+    """dB of a batch-broadcast B: sum_z A[z]^T dC[z] in one launch."""
+    bm = W.bmm(batch=3, m=96, k=80, n=72, seed=1)
+    a, dc = bm["a"], bm["dc"]
+    da, ddc = C.Buffer.of(a), C.Buffer.of(dc)
+    out = C.Buffer((80, 72))
+    C.check(C.lib().vc_hip_matmul_reduce(da.ptr, ddc.ptr, out.ptr, 80, 96, 72, 3, 96 * 80, 96 * 72, 1, 0))
+    expected = K.reduce_axis(K.matmul(a, dc, True, False), 0, K.SUM)
+    np.testing.assert_allclose(out.numpy(), expected, rtol=1e-4, atol=1e-4 * np.sqrt(3 * 96))
+
+
+def binary_dev(a, b, op):
+    a, b = K.f32(a), K.f32(b)
+    shape = K.broadcast_shape(a.shape, b.shape)
+    da, db, dy = C.Buffer.of(a), C.Buffer.of(b), C.Buffer(shape)
+    sa = [int(np.prod(a.shape[i + 1:])) for i in range(a.ndim)]
+    sb = [int(np.prod(b.shape[i + 1:])) for i in range(b.ndim)]
+    C.check(C.lib().vc_hip_binary(da.ptr, C.sizes(a.shape), C.sizes(sa), a.ndim, db.ptr, C.sizes(b.shape),
+                                  C.sizes(sb), b.ndim, dy.ptr, C.sizes(shape), len(shape), op))
+    return dy.numpy()
+
+
+BROADCAST_CASES = [((1000, 300), (1000, 300)), ((1000, 300), ()), ((), (1000, 300)), ((1000, 300), (300,)),
+                   ((1000, 300), (1000, 1)), ((1000, 1), (1, 300)), ((40, 1, 300), (1, 50, 300)),
+                   ((40, 50, 1), (50, 7)), ((3,), (2, 1)), ((4096, 4096), (1, 4096)), ((7, 9), (7, 9))]
+
+
+@pytest.mark.parametrize("a_shape,b_shape", BROADCAST_CASES)
+def test_binary_bitexact(a_shape, b_shape):
+    rng = np.random.default_rng(len(a_shape) * 13 + len(b_shape))
+    a = rng.uniform(0.5, 2, size=a_shape).astype(np.float32)
+    b = rng.uniform(0.5, 2, size=b_shape).astype(np.float32)
+    for op in (C.ADD, C.SUB, C.MUL, C.DIV):
+        np.testing.assert_array_equal(binary_dev(a, b, op), K.binary(a, b, op), err_msg=f"op {op}")
+
+
+def test_binary_scalar_operand_bitexact():
+    x = np.random.default_rng(4).standard_normal(10_001).astype(np.float32)
+    dx, dy = C.Buffer.of(x), C.Buffer(x.shape)
+    for op in (C.ADD, C.SUB, C.MUL, C.DIV):
+        for first in (0, 1):
+            C.check(C.lib().vc_hip_binary_scalar(dx.ptr, x.size, ctypes.c_float(0.1), first, dy.ptr, op))
+            s = np.float32(0.1)
+            expected = K.binary(s, x, op) if first else K.binary(x, s, op)
+            np.testing.assert_array_equal(dy.numpy(), expected)
+
+
+def unary_dev(x, op):
+    dx, dy = C.Buffer.of(x), C.Buffer(x.shape)
+    C.check(C.lib().vc_hip_unary(dx.ptr, dy.ptr, x.size, op))
+    return dy.numpy()
+
+
+def test_unary_against_oracle():
+    x = np.random.default_rng(3).uniform(-5, 5, size=(700, 301)).astype(np.float32)
+    x[0, :4] = [0.0, -0.0, np.nan, np.inf]
+    for op in (C.NEG, C.RELU, C.RELU_GRAD):
+        np.testing.assert_array_equal(unary_dev(x, op), K.unary(x, op))
+    for op in (C.SIGMOID, C.EXP):
+        np.testing.assert_allclose(unary_dev(x, op), K.unary(x, op), rtol=1e-5, atol=0)
+    pos = np.abs(x[1:]) + np.float32(1e-3)
+    np.testing.assert_allclose(unary_dev(pos, C.LOG), K.unary(pos, C.LOG), rtol=1e-5, atol=1e-7)
+
+
+def test_fused_activation_gradients_bitexact():
+    rng = np.random.default_rng(5)
+    g = rng.standard_normal(100_003).astype(np.float32)
+    x = rng.standard_normal(100_003).astype(np.float32)
+    x[:3] = [0.0, -0.0, np.nan]
+    y = K.unary(x, K.SIGMOID)
+    pos = np.abs(x) + np.float32(0.5)
+    dg, dx, dy, dpos, out = C.Buffer.of(g), C.Buffer.of(x), C.Buffer.of(y), C.Buffer.of(pos), C.Buffer(g.shape)
+    L = C.lib()
+    C.check(L.vc_hip_relu_backward(dg.ptr, dx.ptr, out.ptr, g.size))
+    np.testing.assert_array_equal(out.numpy(), K.binary(g, K.unary(x, K.RELU_GRAD), K.MUL))
+    C.check(L.vc_hip_sigmoid_backward(dg.ptr, dy.ptr, out.ptr, g.size))
+    np.testing.assert_array_equal(out.numpy(), K.binary(K.binary(g, y, K.MUL), K.binary(np.float32(1), y, K.SUB), K.MUL))
+    C.check(L.vc_hip_exp_backward(dg.ptr, dy.ptr, out.ptr, g.size))
+    np.testing.assert_array_equal(out.numpy(), K.binary(g, y, K.MUL))
+    C.check(L.vc_hip_log_backward(dg.ptr, dpos.ptr, out.ptr, g.size))
+    np.testing.assert_array_equal(out.numpy(), K.binary(g, pos, K.DIV))
+
+
+def test_div_backward_bitexact_with_broadcast():
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((37, 45)).astype(np.float32)
+    b = rng.uniform(1, 2, size=(45,)).astype(np.float32)
+    g = rng.standard_normal((37, 45)).astype(np.float32)
+    da, db, dg = C.Buffer.of(a), C.Buffer.of(b), C.Buffer.of(g)
+    ga, gb = C.Buffer(g.shape), C.Buffer(g.shape)
+    C.check(C.lib().vc_hip_div_backward(dg.ptr, da.ptr, C.sizes(a.shape), C.sizes([45, 1]), 2, db.ptr, C.sizes([45]),
+                                        C.sizes([1]), 1, C.sizes(g.shape), 2, ga.ptr, gb.ptr))
+    np.testing.assert_array_equal(ga.numpy(), K.binary(g, b, K.DIV))
+    expected_gb = K.binary(K.unary(K.binary(g, a, K.MUL), K.NEG), K.binary(b, b, K.MUL), K.DIV)
+    np.testing.assert_array_equal(gb.numpy(), expected_gb)
+
+
+def test_axpy_matches_sgd_bitexact():
+    rng = np.random.default_rng(7)
+    p = rng.standard_normal(25_001).astype(np.float32)
+    g = rng.standard_normal(25_001).astype(np.float32)
+    dp, dg = C.Buffer.of(p), C.Buffer.of(g)
+    C.check(C.lib().vc_hip_axpy(dp.ptr, dg.ptr, p.size, ctypes.c_float(-0.01)))
+    expected = p.copy()
+    K.sgd_(expected, g, 0.01)
+    np.testing.assert_array_equal(dp.numpy(), expected)
+
+
+def reduce_axis_dev(x, axis, op):
+    _, outer, length, inner, _, removed = K.split_axis(x.shape, axis)
+    dx, dy = C.Buffer.of(x), C.Buffer(removed)
+    C.check(C.lib().vc_hip_reduce_axis(dx.ptr, dy.ptr, outer, length, inner, op))
+    return dy.numpy()
+
+
+@pytest.mark.parametrize("shape", [(64, 500, 33), (5, 300, 7), (4096, 4096), (8192, 1000), (3, 4, 5), (1, 3_000_001),
+                                   (8, 1024 * 1024)])
+def test_reduce_axis_against_oracle(shape):
+    rng = np.random.default_rng(len(shape) + shape[-1])
+    x = rng.standard_normal(shape).astype(np.float32)
+    for axis in range(len(shape)):
+        got = reduce_axis_dev(x, axis, C.SUM)
+        want = K.reduce_axis(x, axis, K.SUM)
+        np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+        if x.shape[axis] <= 100_000:
+            np.testing.assert_array_equal(reduce_axis_dev(x, axis, C.MAX), K.reduce_axis(x, axis, K.MAX))
+            np.testing.assert_array_equal(reduce_axis_dev(x, axis, C.ARGMAX), K.reduce_axis(x, axis, K.ARGMAX))
+
+
+def test_reduce_axis_nan_and_ties_match_reference_fixture(golden):
+    x = golden["reduce_x"]
+    for axis in (0, 1, 2):
+        np.testing.assert_array_equal(reduce_axis_dev(x, axis, C.MAX), golden[f"reduce_max_{axis}"])
+        np.testing.assert_array_equal(reduce_axis_dev(x, axis, C.ARGMAX), golden[f"reduce_argmax_{axis}"])
+        np.testing.assert_allclose(reduce_axis_dev(x, axis, C.SUM), golden[f"reduce_sum_{axis}"], rtol=1e-6)
+    ties = np.array([[1, 3, 3], [2, 2, 0], [np.nan, 5, 1], [0, np.nan, -1]], dtype=np.float32)
+    np.testing.assert_array_equal(reduce_axis_dev(ties, 1, C.ARGMAX), [1, 0, 0, 0])
+
+
+def test_reductions_are_deterministic():
+    x = np.random.default_rng(8).standard_normal((4096, 4096)).astype(np.float32)
+    dx, dy = C.Buffer.of(x), C.Buffer((4096,))
+    runs = []
+    for _ in range(3):
+        C.check(C.lib().vc_hip_reduce_axis(dx.ptr, dy.ptr, 1, 4096, 4096, C.SUM))
+        runs.append(dy.numpy())
+    assert all(np.array_equal(runs[0], r) for r in runs[1:])
+    s = C.Buffer((1,))
+    sums = set()
+    for _ in range(3):
+        C.check(C.lib().vc_hip_reduce_sum(dx.ptr, x.size, s.ptr))
+        sums.add(float(s.numpy()[0]))
+    assert len(sums) == 1
+    assert np.isclose(sums.pop(), K.sum_all(x), rtol=1e-6, atol=1e-3)
+
+
+def test_reduce_sum_edges():
+    for n in (0, 1, 3, 1025, 300_001):
+        x = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+        dx, s = C.Buffer.of(x) if n else C.Buffer((1,)), C.Buffer((1,))
+        C.check(C.lib().vc_hip_reduce_sum(dx.ptr, n, s.ptr))
+        np.testing.assert_allclose(s.numpy()[0], K.sum_all(x), rtol=1e-6, atol=1e-6)
+
+
+def test_scatter_and_transpose_exact():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((6, 40, 9)).astype(np.float32)
+    idx = K.reduce_axis(x, 1, K.ARGMAX)
+    vals = rng.standard_normal((6, 9)).astype(np.float32)
+    dv, di, do = C.Buffer.of(vals), C.Buffer.of(idx), C.Buffer(x.shape)
+    C.check(C.lib().vc_hip_scatter_axis(dv.ptr, di.ptr, do.ptr, 6, 40, 9))
+    np.testing.assert_array_equal(do.numpy(), K.scatter_axis(vals, idx, x.shape, 1))
+    for shape in [(2, 3, 4), (1, 1000, 300), (5, 33, 65)]:
+        t = rng.standard_normal(shape).astype(np.float32)
+        dt, dout = C.Buffer.of(t), C.Buffer(shape[:-2] + (shape[-1], shape[-2]))
+        C.check(C.lib().vc_hip_transpose_last2(dt.ptr, dout.ptr, shape[0], shape[1], shape[2]))
+        np.testing.assert_array_equal(dout.numpy(), K.transpose_last2(t))
+
+
+def xent_dev(logits, targets):
+    rows, classes = logits.shape
+    dl, dt = C.Buffer.of(logits), C.Buffer.of(targets.astype(np.int32), dtype=np.int32)
+    stats, loss = C.Buffer((rows, 2)), C.Buffer((1,))
+    C.check(C.lib().vc_hip_xent_forward(dl.ptr, dt.ptr, rows, classes, stats.ptr, loss.ptr))
+    one = C.Buffer.of(np.ones(1, dtype=np.float32))
+    grad = C.Buffer(logits.shape)
+    C.check(C.lib().vc_hip_xent_backward(dl.ptr, dt.ptr, stats.ptr, one.ptr, rows, classes, grad.ptr))
+    return loss.numpy()[0], grad.numpy()
+
+
+def test_cross_entropy_matches_reference_fixture(golden):
+    loss, grad = xent_dev(golden["xent_logits"], golden["xent_targets"])
+    np.testing.assert_allclose(loss, golden["xent_loss"], rtol=1e-6)
+    np.testing.assert_allclose(grad, golden["xent_grad"], rtol=1e-5, atol=1e-9)
+
+
+@pytest.mark.parametrize("rows,classes", [(512, 1000), (300, 3), (64, 37), (4, 2)])
+def test_cross_entropy_against_oracle(rows, classes):
+    from oracle import autograd as A
+    xe = W.xent(rows=rows, classes=classes, seed=rows + classes)
+    loss, grad = xent_dev(xe["logits"], xe["targets"])
+    t = A.T(xe["logits"], True)
+    ref_loss = A.cross_entropy(t, xe["targets"])
+    ref_loss.backward()
+    np.testing.assert_allclose(loss, ref_loss.data, rtol=1e-6)
+    np.testing.assert_allclose(grad, t.grad.data, rtol=1e-5, atol=1e-9)
+
+
+def test_pool_reuses_released_buffers():
+    before = C.pool_stats()
+    bufs = [C.Buffer((1 << 20,)) for _ in range(4)]
+    for b in bufs:
+        b.release()
+    mid = C.pool_stats()
+    bufs = [C.Buffer((1 << 20,)) for _ in range(4)]
+    after = C.pool_stats()
+    assert after.device_allocations == mid.device_allocations
+    assert after.reuses >= mid.reuses + 4
+    assert mid.device_allocations <= before.device_allocations + 4
+    for b in bufs:
+        b.release()
+
+
+def test_errors_are_reported_not_thrown():
+    with pytest.raises(ValueError):
+        C.check(C.lib().vc_hip_unary(None, None, 4, 99))
+    with pytest.raises(ValueError):
+        C.check(C.lib().vc_hip_reduce_axis(None, None, 1, 0, 1, C.MAX))
+    assert b"empty axis" in C.lib().vc_hip_last_error()

@@ -1,0 +1,126 @@
+// Internal plumbing shared by the HIP translation units of libvc_hip.so:
+// the device singleton (one in-order stream), status/error reporting, launch
+// checks and the optional per-launch event profiler.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "vc_hip.h"
+
+namespace vchip {
+
+// An error carrying the C-ABI status it maps to.
+struct Error : std::runtime_error {
+    int status;
+    Error(int s, const std::string& message) : std::runtime_error(message), status(s) {}
+};
+
+[[noreturn]] inline void fail(int status, const std::string& message) { throw Error(status, message); }
+
+inline void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        fail(e == hipErrorOutOfMemory ? VC_HIP_ERR_OUT_OF_MEMORY : VC_HIP_ERR_RUNTIME,
+             std::string(what) + ": " + hipGetErrorString(e));
+    }
+}
+
+void set_last_error(const std::string& message);
+
+// Runs `body` and converts exceptions into a status + thread-local message.
+template <typename F>
+int guard(F&& body) {
+    try {
+        body();
+        return VC_HIP_OK;
+    } catch (const Error& e) {
+        set_last_error(e.what());
+        return e.status;
+    } catch (const std::bad_alloc&) {
+        set_last_error("host allocation failed");
+        return VC_HIP_ERR_OUT_OF_MEMORY;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return VC_HIP_ERR_RUNTIME;
+    }
+}
+
+struct Device {
+    bool ready = false;
+    std::string error;  // why the device is unavailable
+    std::string name;
+    int ordinal = 0;
+    int cu_count = 0;
+    hipStream_t stream = nullptr;
+    bool sync_each_launch = false;  // VECTORCORE_HIP_SYNC_EACH=1 (fault localisation)
+    bool simple_gemm = false;       // VECTORCORE_HIP_GEMM=simple
+};
+
+// Initialises once (thread-safe) and makes the device current on this thread.
+Device& device();
+// device() plus a thrown VC_HIP_ERR_UNAVAILABLE when there is no usable GPU.
+Device& require_device();
+
+// Call right after every kernel launch on the library stream.
+void after_launch(const char* label);
+
+// Pool-backed device scratch for multi-pass kernels. Released to the pool when
+// the object dies; stream order keeps the enqueued passes safe.
+void* pool_alloc(size_t bytes);
+void pool_release(void* p) noexcept;
+class Scratch {
+public:
+    explicit Scratch(size_t bytes) : p_(pool_alloc(bytes)) {}
+    ~Scratch() { pool_release(p_); }
+    Scratch(const Scratch&) = delete;
+    Scratch& operator=(const Scratch&) = delete;
+    template <typename T>
+    T* as() const { return static_cast<T*>(p_); }
+private:
+    void* p_;
+};
+
+// --- profiler --------------------------------------------------------------
+// Usage around one launch:  Profiled p("label", flops, bytes);  kernel<<<...>>>;
+// p.done();  Both are no-ops unless profiling is enabled.
+class Profiled {
+public:
+    Profiled(const char* label, double flops, double bytes);
+    void done();
+private:
+    int label_ = -1;
+    hipEvent_t start_ = nullptr, stop_ = nullptr;
+    double flops_ = 0, bytes_ = 0;
+};
+
+// --- launch-shape checks -----------------------------------------------------
+inline unsigned grid_1d(size_t items, unsigned block, unsigned max_blocks) {
+    size_t blocks = (items + block - 1) / block;
+    if (blocks == 0) blocks = 1;
+    if (blocks > max_blocks) blocks = max_blocks;
+    return static_cast<unsigned>(blocks);
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Shape metadata for broadcasting kernels (rank <= 8), passed by value.
+constexpr int kMaxRank = 8;
+struct Bcast {
+    int rank;
+    int64_t out_shape[kMaxRank];
+    int64_t a_stride[kMaxRank];  // 0 on broadcast axes
+    int64_t b_stride[kMaxRank];
+};
+
+// Builds collapsed broadcast metadata; throws VC_HIP_ERR_INVALID_ARGUMENT for
+// a rank above 8 or incompatible shapes.
+Bcast make_bcast(const size_t* a_shape, const size_t* a_strides, size_t a_rank, const size_t* b_shape,
+                 const size_t* b_strides, size_t b_rank, const size_t* out_shape, size_t out_rank);
+
+}  // namespace vchip

@@ -1,0 +1,220 @@
+// Fused softmax cross-entropy loss node (the hip path of src/nn.cpp:31-53).
+//
+// The reference composes the loss from ~10 tensor ops over [rows, classes]:
+//   m = max(x, 1) (detached), shifted = x - m, s = sum(exp(shifted), 1)
+//   (double accumulation), logsm = shifted - log(s),
+//   loss = -(sum(logsm * onehot)) / rows                    (src/ops.cpp:378-384)
+// and its backward walks the same graph in reverse. With c = g / rows that
+// backward evaluates, per element,
+//   dx_ij = ((c / s_i) * exp(x_ij - m_i)) + (j == t_i ? -c : -0.0)
+// (div -> negate -> sum -> mul -> sub/log/sum/exp rules of src/ops.cpp). These
+// kernels compute exactly those fp32 operations, in that order, reading the
+// logits once per pass: one wavefront per row, lanes striding the classes,
+// row statistics combined with cross-lane shuffles.
+//
+// The reference's masked sum also turns any non-finite non-target log-prob
+// into NaN (inf * 0); the forward reproduces that.
+#include "vc_hip_internal.hpp"
+
+#include <algorithm>
+#include <limits>
+
+namespace vchip {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr unsigned kBlock = 256;
+constexpr int kRowsPerBlock = kBlock / kWave;
+constexpr int kNone = std::numeric_limits<int>::max();
+
+__device__ inline f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+
+struct Best {
+    float v;
+    int i;
+};
+__device__ inline void consider(Best& b, float v, int i) {
+    if (v != v) return;
+    if (b.i == kNone || v > b.v || (v == b.v && i < b.i)) {
+        b.v = v;
+        b.i = i;
+    }
+}
+__device__ inline Best combine(Best a, Best b) {
+    if (b.i == kNone) return a;
+    if (a.i == kNone) return b;
+    return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
+}
+
+__device__ inline float row_max(const float* row, int64_t len, int lane, bool vec) {
+    Best b{0.0f, kNone};
+    if (vec) {
+        for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
+            const f4 v = ld4(row + a);
+            consider(b, v.x, int(a));
+            consider(b, v.y, int(a + 1));
+            consider(b, v.z, int(a + 2));
+            consider(b, v.w, int(a + 3));
+        }
+    } else {
+        for (int64_t a = lane; a < len; a += kWave) consider(b, row[a], int(a));
+    }
+    for (int off = kWave / 2; off > 0; off >>= 1) b = combine(b, Best{__shfl_xor(b.v, off, kWave), __shfl_xor(b.i, off, kWave)});
+    const float first = row[0];
+    return first != first ? first : b.v;  // max() keeps a NaN first element (src/cpu/cpu_backend.cpp:443-452)
+}
+
+template <bool Vec>
+__global__ __launch_bounds__(kBlock) void xent_rows_kernel(const float* __restrict__ x, const int* __restrict__ targets,
+                                                           int64_t rows, int64_t len, float* __restrict__ stats,
+                                                           float* __restrict__ terms) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t r = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
+    if (r >= rows) return;
+    const float* row = x + r * len;
+    const float m = row_max(row, len, lane, Vec);
+    const int t = targets[r];
+    double acc = 0.0;
+    int bad = 0;  // a non-target log-prob that is not finite
+    if (Vec) {
+        for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
+            const f4 v = ld4(row + a);
+            const float s0 = v.x - m, s1 = v.y - m, s2 = v.z - m, s3 = v.w - m;
+            acc += double(expf(s0));
+            acc += double(expf(s1));
+            acc += double(expf(s2));
+            acc += double(expf(s3));
+            bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) | (a + 2 != t && !isfinite(s2)) |
+                   (a + 3 != t && !isfinite(s3));
+        }
+    } else {
+        for (int64_t a = lane; a < len; a += kWave) {
+            const float s = row[a] - m;
+            acc += double(expf(s));
+            bad |= (a != t && !isfinite(s));
+        }
+    }
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        acc += __shfl_xor(acc, off, kWave);
+        bad |= __shfl_xor(bad, off, kWave);
+    }
+    if (lane == 0) {
+        const float s = float(acc);
+        const float L = logf(s);
+        float term;
+        if (t < 0 || int64_t(t) >= len) {
+            term = __builtin_nanf("");  // never reached with checked targets; no out-of-row read
+        } else {
+            const float shifted = row[t] - m;
+            term = bad ? __builtin_nanf("") : shifted - L;
+        }
+        stats[2 * r] = m;
+        stats[2 * r + 1] = s;
+        terms[r] = term;
+    }
+}
+
+// loss = -(float)(sum terms) / (float)rows, the sum in double over a fixed tree.
+__global__ __launch_bounds__(kBlock) void xent_loss_kernel(const float* __restrict__ terms, int64_t rows,
+                                                           float* __restrict__ loss) {
+    __shared__ double lds[kBlock / kWave];
+    double acc = 0.0;
+    for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) acc += double(terms[r]);
+    for (int off = kWave / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+    if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double total = 0.0;
+        for (int w = 0; w < int(blockDim.x / kWave); ++w) total += lds[w];
+        const float sum = float(total);
+        const float negated = -sum;
+        loss[0] = negated / float(rows);
+    }
+}
+
+template <bool Vec>
+__global__ __launch_bounds__(kBlock) void xent_backward_kernel(const float* __restrict__ x, const int* __restrict__ targets,
+                                                               const float* __restrict__ stats,
+                                                               const float* __restrict__ grad_loss, int64_t rows,
+                                                               int64_t len, float* __restrict__ dx) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t r = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
+    if (r >= rows) return;
+    const float c = grad_loss[0] / float(rows);
+    const float m = stats[2 * r], s = stats[2 * r + 1];
+    const float scale = c / s;
+    const float neg_c = -c;
+    const int t = targets[r];
+    const float* row = x + r * len;
+    float* out = dx + r * len;
+    if (Vec) {
+        for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
+            const f4 v = ld4(row + a);
+            f4 g;
+            g.x = scale * expf(v.x - m) + (a == t ? neg_c : -0.0f);
+            g.y = scale * expf(v.y - m) + (a + 1 == t ? neg_c : -0.0f);
+            g.z = scale * expf(v.z - m) + (a + 2 == t ? neg_c : -0.0f);
+            g.w = scale * expf(v.w - m) + (a + 3 == t ? neg_c : -0.0f);
+            *reinterpret_cast<f4*>(out + a) = g;
+        }
+    } else {
+        for (int64_t a = lane; a < len; a += kWave) out[a] = scale * expf(row[a] - m) + (a == t ? neg_c : -0.0f);
+    }
+}
+
+}  // namespace
+}  // namespace vchip
+
+using namespace vchip;
+
+extern "C" {
+
+int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows, size_t classes, float* row_stats,
+                        float* loss) {
+    return guard([&] {
+        Device& d = require_device();
+        if (rows == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "cross_entropy of an empty batch is undefined");
+        if (classes == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "cross_entropy needs at least one class");
+        if (classes > size_t(std::numeric_limits<int>::max())) fail(VC_HIP_ERR_OVERFLOW, "too many classes");
+        const int64_t R = int64_t(rows), C = int64_t(classes);
+        Scratch terms(rows * sizeof(float));
+        const bool vec = C % 4 == 0 && aligned16(logits);
+        const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
+        Profiled p("xent_forward", 0.0, 4.0 * double(R * C) + 4.0 * double(R) + 8.0 * double(R));
+        if (vec)
+            hipLaunchKernelGGL(xent_rows_kernel<true>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, R, C, row_stats,
+                               terms.as<float>());
+        else
+            hipLaunchKernelGGL(xent_rows_kernel<false>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, R, C,
+                               row_stats, terms.as<float>());
+        after_launch("xent_forward");
+        hipLaunchKernelGGL(xent_loss_kernel, dim3(1), dim3(kBlock), 0, d.stream, terms.as<float>(), R, loss);
+        after_launch("xent_forward");
+        p.done();
+    });
+}
+
+int vc_hip_xent_backward(const float* logits, const int32_t* targets, const float* row_stats, const float* grad_loss,
+                         size_t rows, size_t classes, float* grad_logits) {
+    return guard([&] {
+        Device& d = require_device();
+        if (rows == 0 || classes == 0) return;
+        if (classes > size_t(std::numeric_limits<int>::max())) fail(VC_HIP_ERR_OVERFLOW, "too many classes");
+        const int64_t R = int64_t(rows), C = int64_t(classes);
+        const bool vec = C % 4 == 0 && aligned16(logits) && aligned16(grad_logits);
+        const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
+        Profiled p("xent_backward", 0.0, 8.0 * double(R * C) + 12.0 * double(R));
+        if (vec)
+            hipLaunchKernelGGL(xent_backward_kernel<true>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, row_stats,
+                               grad_loss, R, C, grad_logits);
+        else
+            hipLaunchKernelGGL(xent_backward_kernel<false>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets,
+                               row_stats, grad_loss, R, C, grad_logits);
+        after_launch("xent_backward");
+        p.done();
+    });
+}
+
+}  // extern "C"

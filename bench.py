@@ -1,0 +1,212 @@
+#!/usr/bin/env python3
+"""Train-step benchmark of the MI355X backend.
+
+Workload: one SGD train step of the fp32 MLP 8192 x 1024 -> 4096 -> 4096 -> 1000
+(ReLU between layers, softmax cross-entropy over int targets, full reverse-mode
+backward through the autograd graph, SGD at lr 0.01; W ~ U(+-1/sqrt(fan_in)),
+biases 0, x ~ N(0, 1), seed 4), all on the hip device with inputs resident in
+HBM. Each step ends with loss.item(), as the reference's train benchmark does
+(benchmarks/train_benchmark.py:43-48). Parameter, activation and gradient
+buffers are recycled through the device pool.
+
+Prints one JSON line: whole-job train-steps/s, the backward-GEMM roofline
+(MFMA-bound; per-launch HIP events on the library stream over the timed
+region), the reduction bandwidth, and the reference CPU path timed on this
+host on a bounded slice of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+DIMS = (1024, 4096, 4096, 1000)
+BATCH = 8192
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+CPU_SAMPLE_ROWS = 1024         # CPU baseline: 1/8 of the batch, same network
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def gpu_bench(steps: int, warmup: int):
+    import numpy as np
+
+    import vectorcore_amd as vc
+    from vectorcore_amd import workloads as W
+
+    if not vc.hip_available():
+        raise SystemExit("bench.py: the hip device is unavailable: the MI355X backend needs a gfx950 GPU")
+    m = W.mlp(batch=BATCH, dims=DIMS)
+    params = []
+    for w, b in zip(m["weights"], m["biases"]):
+        params += [vc.Tensor(w, requires_grad=True, device="hip"), vc.Tensor(b, requires_grad=True, device="hip")]
+    x = vc.Tensor(m["x"], device="hip")
+    targets = m["targets"]
+    lr = m["lr"]
+
+    def step():
+        h = x
+        for i in range(3):
+            h = h @ params[2 * i] + params[2 * i + 1]
+            if i < 2:
+                h = h.relu()
+        loss = vc.cross_entropy(h, targets)
+        loss.backward()
+        vc.sgd_step(params, lr)
+        vc.zero_grad(params)
+        return loss.item()
+
+    losses = [step() for _ in range(warmup)]
+    allocs_before = vc.hip_pool_stats()["device_allocations"]
+    vc.synchronize()
+    vc.hip_profile(True)
+    vc.hip_profile_reset()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        losses.append(step())
+    vc.synchronize()
+    elapsed = time.perf_counter() - t0
+    prof = vc.hip_profile_read()
+    vc.hip_profile(False)
+    allocs_after = vc.hip_pool_stats()["device_allocations"]
+    if not np.isfinite(losses[-1]) or not losses[-1] < losses[0]:
+        raise SystemExit(f"bench.py: training did not make progress: {losses[0]} -> {losses[-1]}")
+    return dict(elapsed=elapsed, prof=prof, losses=losses, new_allocations=allocs_after - allocs_before,
+                device=vc.hip_device_name(), gemm_kernel=vc.hip_gemm_kernel())
+
+
+def cpu_baseline():
+    """The reference VectorCore (built from its own sources into oracle/_ref)
+    running the same step on this host's cores, on a 1024-row slice of the
+    batch (same network, 1/8 of the work); reported per full-batch step."""
+    import numpy as np
+
+    from oracle import kernels as K
+    from vectorcore_amd import workloads as W
+
+    m = W.mlp(batch=BATCH, dims=DIMS)
+    rows = CPU_SAMPLE_ROWS
+    if K.Reference.available():
+        ref = K.Reference()
+        net = ref.mlp(m["weights"], m["biases"], m["x"][:rows], m["targets"][:rows])
+        net.step(m["lr"])  # warm-up (thread pool, first-touch)
+        times = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            net.step(m["lr"])
+            times.append(time.perf_counter() - t0)
+        per_full_step = float(np.median(times)) * (BATCH / rows)
+        return dict(value=1.0 / per_full_step, unit="train-steps/s", cores=ref.threads(), kind="reference",
+                    sample=f"reference VectorCore CPU path (oracle/_ref, -O3, no -march), {rows}-row slice of the "
+                           f"8192-row batch, same 1024-4096-4096-1000 network, median of 2 steps after 1 warm-up, "
+                           f"scaled x{BATCH // rows} to a full step")
+    from oracle import autograd as A
+    net = A.Mlp(m["weights"], m["biases"])
+    rows = 256
+    x = A.T(m["x"][:rows])
+    t0 = time.perf_counter()
+    net.step(x, m["targets"][:rows], m["lr"])
+    per_full_step = (time.perf_counter() - t0) * (BATCH / rows)
+    return dict(value=1.0 / per_full_step, unit="train-steps/s", cores=os.cpu_count() or 1, kind="port",
+                sample=f"C oracle, {rows}-row slice, one step, scaled x{BATCH // rows}")
+
+
+def load_traffic():
+    """HBM bytes per launch of the dominant kernels, measured with rocprofv3
+    FETCH_SIZE/WRITE_SIZE runs and kept in profiles/ (None when absent)."""
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the data-parallel "
+              "sharding of this workload is a design note, not a launched path)", file=sys.stderr)
+        sys.exit(2)
+
+    r = gpu_bench(args.steps, args.warmup)
+    prof = r["prof"]
+    ms_per_step = r["elapsed"] * 1e3 / args.steps
+    bwd = [v for k, v in prof.items() if k in ("gemm_nt", "gemm_tn")]
+    bwd_flops = sum(v["flops"] for v in bwd)
+    bwd_ms = sum(v["ms"] for v in bwd)
+    bwd_launches = sum(v["launches"] for v in bwd)
+    bwd_tflops = bwd_flops / bwd_ms / 1e9 if bwd_ms else None
+    red = prof.get("reduce_axis_sum", {})
+    reduce_gbs = red["bytes"] / red["ms"] / 1e6 if red.get("ms") else None
+    fwd = prof.get("gemm_nn", {})
+    fwd_tflops = fwd["flops"] / fwd["ms"] / 1e9 if fwd.get("ms") else None
+    device_ms = sum(v["ms"] for v in prof.values()) / args.steps
+    for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
+        rate = (f"{v['flops'] / v['ms'] / 1e9:7.1f} TFLOP/s" if v["flops"] and "gemm" in k
+                else f"{v['bytes'] / v['ms'] / 1e6:7.0f} GB/s")
+        log(f"  {k:22s} {v['launches'] / args.steps:5.1f}/step {v['ms'] / args.steps:8.3f} ms/step  {rate}")
+    log(f"  device time {device_ms:.3f} ms/step of {ms_per_step:.3f} ms/step wall")
+
+    traffic = load_traffic()
+    roofline = {
+        "bound": "mfma",
+        "kernel": "backward GEMMs (gemm_nt dH = dY W^T, gemm_tn dW = H^T dY), fp32 V_MFMA_F32_32X32X2_F32",
+        "achieved": round(bwd_tflops, 2) if bwd_tflops else None,
+        "peak": FP32_MFMA_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(bwd_tflops / FP32_MFMA_PEAK_TFLOPS, 4) if bwd_tflops else None,
+        "traffic": traffic.get("bwd_gemm_bytes_per_launch") if traffic else None,
+        "launches_per_step": bwd_launches / args.steps,
+        "flops_per_step": bwd_flops / args.steps,
+    }
+    out = {
+        "metric": "MLP train-steps/s (8192x1024->4096->4096->1000 fp32); bwd GEMM TFLOP/s; reduce GB/s",
+        "value": round(1e3 / ms_per_step, 3),
+        "unit": "train-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) inputs, U(+-1/sqrt(fan_in)) weights, uniform int targets)",
+        "config": {"workload": "MLP train step: forward, softmax cross-entropy, backward, SGD lr 0.01",
+                   "global_batch": BATCH, "layers": list(DIMS), "parallelism": "single GPU"},
+        "bwd_gemm_tflops": round(bwd_tflops, 2) if bwd_tflops else None,
+        "fwd_gemm_tflops": round(fwd_tflops, 2) if fwd_tflops else None,
+        "reduce_gbs": round(reduce_gbs, 1) if reduce_gbs else None,
+        "reduce_hbm_frac": round(reduce_gbs / HBM_PEAK_GBS, 4) if reduce_gbs else None,
+        "device_ms_per_step": round(device_ms, 3),
+        "pool_new_allocations_in_timed_steps": r["new_allocations"],
+        "loss_first_last": [round(r["losses"][0], 5), round(r["losses"][-1], 5)],
+        "device": r["device"],
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        t0 = time.perf_counter()
+        out["cpu_baseline"] = cpu_baseline()
+        log(f"  cpu baseline took {time.perf_counter() - t0:.1f} s")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

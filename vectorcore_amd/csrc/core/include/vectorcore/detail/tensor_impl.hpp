@@ -1,0 +1,52 @@
+#pragma once
+// Graph and tensor internals (API of include/vectorcore/detail/tensor_impl.hpp).
+#include "vectorcore/shape.hpp"
+#include "vectorcore/storage.hpp"
+#include "vectorcore/tensor.hpp"
+
+#include <functional>
+#include <memory>
+#include <vector>
+
+namespace vectorcore::detail {
+
+struct TensorImpl;
+
+// A node owns its parents (never its children), so graphs have no cycles.
+struct GradFn {
+    std::vector<std::shared_ptr<TensorImpl>> parents;
+    std::function<std::vector<Tensor>(const Tensor&)> backward;
+};
+
+struct TensorImpl {
+    std::shared_ptr<Storage> storage;
+    Shape shape;
+    Strides strides;
+    std::size_t offset{0};
+    DType dtype{DType::Float32};
+    bool requires_grad{false};
+    bool leaf{true};
+    bool retains_grad{false};
+    std::shared_ptr<GradFn> grad_fn;
+    std::shared_ptr<TensorImpl> grad;
+};
+
+// A tensor saved for a backward rule with its storage version; unpack()
+// throws std::runtime_error if the storage was modified in place since.
+class SavedTensor {
+public:
+    explicit SavedTensor(const Tensor& value);
+    [[nodiscard]] Tensor unpack() const;
+private:
+    Tensor tensor_;
+    std::uint64_t version_;
+};
+
+Tensor from_impl(std::shared_ptr<TensorImpl> impl);
+Tensor make_tensor(std::shared_ptr<Storage> storage, Shape shape, bool requires_grad = false);
+void attach_grad_fn(Tensor& output, const std::vector<Tensor>& parents,
+                    std::function<std::vector<Tensor>(const Tensor&)> backward);
+Tensor sum_to_shape(const Tensor& gradient, const Shape& target_shape);
+Tensor broadcast_to(const Tensor& value, const Shape& target_shape);
+
+}  // namespace vectorcore::detail

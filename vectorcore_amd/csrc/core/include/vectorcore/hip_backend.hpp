@@ -1,0 +1,100 @@
+#pragma once
+// The `hip` device: a C++ wrapper over the C ABI of include/vc_hip.h.
+//
+// HipBackend keeps the member set of the reference's device interface
+// (MetalBackend, include/vectorcore/metal_backend.hpp:13-56) so the dispatch
+// sites of ops/tensor/autograd/nn call it the same way, and adds the fused
+// backward kernels that the hip arm of those sites uses. Every member throws
+// the reference's exception types; there is no CPU fallback.
+#include "vectorcore/cpu_backend.hpp"
+#include "vectorcore/shape.hpp"
+#include "vectorcore/storage.hpp"
+
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace vectorcore {
+
+class HipBackend {
+public:
+    static HipBackend& instance();
+
+    [[nodiscard]] bool available() const noexcept;
+    [[nodiscard]] std::string device_name() const;
+    [[nodiscard]] std::string last_error() const;
+    // "mfma" (matrix-core tiles), "simple" (VECTORCORE_HIP_GEMM=simple) or "unavailable".
+    [[nodiscard]] std::string gemm_kernel() const;
+
+    // --- the reference device interface ---
+    [[nodiscard]] std::shared_ptr<Storage> allocate(std::size_t elements);
+    [[nodiscard]] std::shared_ptr<Storage> upload(const float* data, std::size_t elements);
+    void download(const Storage& source, std::size_t offset, float* destination, std::size_t elements);
+    [[nodiscard]] std::shared_ptr<Storage> binary(const Storage& a, std::size_t a_offset, const Shape& a_shape,
+                                                  const Strides& a_strides, const Storage& b, std::size_t b_offset,
+                                                  const Shape& b_shape, const Strides& b_strides,
+                                                  const Shape& out_shape, cpu::BinaryOp operation);
+    [[nodiscard]] std::shared_ptr<Storage> unary(const Storage& input, std::size_t offset, std::size_t count,
+                                                 cpu::UnaryOp operation);
+    // Output z is op(A + a_offsets[z]) @ op(B + b_offsets[z]) (offsets in elements).
+    [[nodiscard]] std::shared_ptr<Storage> matmul(const Storage& a, std::size_t a_offset, const Storage& b,
+                                                  std::size_t b_offset, std::size_t m, std::size_t k, std::size_t n,
+                                                  const std::vector<std::size_t>& a_offsets,
+                                                  const std::vector<std::size_t>& b_offsets, bool trans_a,
+                                                  bool trans_b);
+    [[nodiscard]] std::shared_ptr<Storage> transpose_last2(const Storage& input, std::size_t offset, std::size_t batch,
+                                                           std::size_t rows, std::size_t cols);
+    [[nodiscard]] std::shared_ptr<Storage> reduce_sum(const Storage& input, std::size_t offset, std::size_t count);
+    [[nodiscard]] std::shared_ptr<Storage> reduce_axis(const Storage& input, std::size_t offset, std::size_t outer,
+                                                       std::size_t length, std::size_t inner, cpu::ReduceOp operation);
+    [[nodiscard]] std::shared_ptr<Storage> scatter_axis(const Storage& values, std::size_t values_offset,
+                                                        const Storage& indices, std::size_t indices_offset,
+                                                        std::size_t outer, std::size_t length, std::size_t inner);
+    void axpy_inplace(Storage& target, std::size_t target_offset, const Storage& source, std::size_t source_offset,
+                      std::size_t count, float alpha);
+    void synchronize();
+
+    // --- fused kernels used by the hip arm of the backward rules ---
+    [[nodiscard]] std::shared_ptr<Storage> fill(std::size_t count, float value);
+    // out = a op s (scalar_first false) or s op a; s is a host value.
+    [[nodiscard]] std::shared_ptr<Storage> binary_scalar(const Storage& a, std::size_t a_offset, std::size_t count,
+                                                         float s, bool scalar_first, cpu::BinaryOp operation);
+    // The broadcast-batch gradient: sum_z op(A + z*a_stride) @ op(B + z*b_stride).
+    [[nodiscard]] std::shared_ptr<Storage> matmul_reduce(const Storage& a, std::size_t a_offset, const Storage& b,
+                                                         std::size_t b_offset, std::size_t m, std::size_t k,
+                                                         std::size_t n, std::size_t count, std::size_t a_stride,
+                                                         std::size_t b_stride, bool trans_a, bool trans_b);
+    enum class Activation { Relu, Sigmoid, Exp, Log };
+    // relu: grad * [input > 0]; sigmoid: (grad * y) * (1 - y); exp: grad * y; log: grad / input.
+    [[nodiscard]] std::shared_ptr<Storage> activation_backward(Activation kind, const Storage& grad,
+                                                               std::size_t grad_offset, const Storage& saved,
+                                                               std::size_t saved_offset, std::size_t count);
+    // Division gradients over out_shape: {grad / b, -(grad * a) / (b * b)} (either may be skipped).
+    std::pair<std::shared_ptr<Storage>, std::shared_ptr<Storage>> divide_backward(
+        const Storage& grad, std::size_t grad_offset, const Storage& a, std::size_t a_offset, const Shape& a_shape,
+        const Strides& a_strides, const Storage& b, std::size_t b_offset, const Shape& b_shape,
+        const Strides& b_strides, const Shape& out_shape, bool need_a, bool need_b);
+    // Class indices as int32 on the device (caller has range-checked them).
+    [[nodiscard]] std::shared_ptr<Storage> upload_targets(const std::vector<std::size_t>& targets);
+    // Returns {loss (1 element), row statistics (2 per row)}.
+    std::pair<std::shared_ptr<Storage>, std::shared_ptr<Storage>> cross_entropy_forward(
+        const Storage& logits, std::size_t logits_offset, const Storage& targets, std::size_t rows,
+        std::size_t classes);
+    [[nodiscard]] std::shared_ptr<Storage> cross_entropy_backward(const Storage& logits, std::size_t logits_offset,
+                                                                  const Storage& targets, const Storage& row_stats,
+                                                                  const Storage& grad_loss, std::size_t grad_offset,
+                                                                  std::size_t rows, std::size_t classes);
+};
+
+// Host-side value of a one-element hip storage created from host data, if it
+// has not been written on the device since (lets scalar operands skip a
+// device read).
+std::optional<float> hip_host_scalar(const Storage& storage);
+
+[[nodiscard]] bool hip_available();
+[[nodiscard]] std::string hip_device_name();
+
+}  // namespace vectorcore

@@ -83,6 +83,7 @@ __device__ inline void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, i
 
 // Buffer resource over `base` (gfx9 descriptor word 3). Offsets at or above
 // kOutOfRange fall outside num_records: loads return 0, stores are dropped.
+// The raw buffer builtins move 32-bit integers; values are bit-cast.
 constexpr uint32_t kOutOfRange = 0x80000000u;
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), short(0), int(kOutOfRange - 1), 0x00020000);
@@ -135,7 +136,7 @@ struct TileLoader {
         for (int q = 0; q < 4; ++q) {
             if (Vec) {
                 const bool ok = ((mn_ok >> q) & 1) && (k0 + kpos[q] < K);
-                reg[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? boff[q] : kOutOfRange, 0, 0);
+                reg[q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? boff[q] : kOutOfRange, 0, 0));
             } else {
                 const int idx = threadIdx.x + q * kThreads;
                 f4 v;
@@ -151,7 +152,7 @@ struct TileLoader {
                     }
                     const bool ok = mn < mn_lim && k0 + k < K;
                     const uint32_t off = uint32_t(KC ? mn * ld + k : k * ld + mn) * 4u;
-                    v[e] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? off : kOutOfRange, 0, 0);
+                    v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? off : kOutOfRange, 0, 0));
                 }
                 reg[q] = v;
             }
@@ -267,7 +268,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
                 for (int v = 0; v < 16; ++v) {
                     const int row = row0 + 32 * i + 8 * (v >> 2) + (v & 3);
                     const bool ok = row < row_lim && col < col_lim;
-                    __builtin_amdgcn_raw_buffer_store_b32(acc[i][j][v], rc, ok ? uint32_t(row * p.N + col) * 4u : kOutOfRange,
+                    const float value = acc[i][j][v];  // element first: bit-casting the subscript takes lane 0
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), rc,
+                                                          ok ? uint32_t(row * p.N + col) * 4u : kOutOfRange,
                                                           0, 0);
                 }
             }

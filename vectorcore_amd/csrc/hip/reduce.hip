@@ -13,6 +13,7 @@
 // the axis is split across lanes, each part keeps the best non-NaN
 // (value, index) with ties going to the smaller index, and the first element
 // is checked for NaN at the end; that reproduces the scan exactly.
+#include "reduce_common.hpp"
 #include "vc_hip_internal.hpp"
 
 #include <algorithm>
@@ -21,13 +22,12 @@
 namespace vchip {
 namespace {
 
-typedef float f4 __attribute__((ext_vector_type(4)));
+using red::f4;
+using red::kBlock;
+using red::kWave;
+using red::ld4;
 
-constexpr int kWave = 64;
-constexpr unsigned kBlock = 256;
 constexpr int kNone = std::numeric_limits<int>::max();  // "no candidate yet"
-
-__device__ inline f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 
 struct Best {
     float v;
@@ -48,11 +48,6 @@ __device__ inline Best combine(Best a, Best b) {
     return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
 }
 
-__device__ inline double wave_sum(double v) {
-    for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
-
 __device__ inline Best wave_best(Best b) {
     for (int off = kWave / 2; off > 0; off >>= 1) {
         Best o{__shfl_xor(b.v, off, kWave), __shfl_xor(b.i, off, kWave)};
@@ -62,7 +57,7 @@ __device__ inline Best wave_best(Best b) {
 }
 
 // ---- rows: inner == 1, one wavefront per row -----------------------------------
-// op: 0 sum, 1 max, 2 argmax.
+// Op: 0 sum, 1 max, 2 argmax.
 template <int Op, bool Vec>
 __global__ __launch_bounds__(kBlock) void rows_kernel(const float* __restrict__ x, float* __restrict__ out, int64_t rows,
                                                       int64_t len) {
@@ -83,7 +78,7 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(const float* __restrict__ 
             } else {
                 for (int64_t a = lane; a < len; a += kWave) acc += double(row[a]);
             }
-            acc = wave_sum(acc);
+            acc = red::wave_sum(acc);
             if (lane == 0) out[r] = float(acc);
         } else {
             Best b{0.0f, kNone};
@@ -109,7 +104,8 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(const float* __restrict__ 
 }
 
 // ---- columns: inner > 1, one thread per output, sequential along the axis -------
-// Walks the axis in order exactly like the reference loop.
+// Walks the axis in order exactly like the reference loop; used when there
+// are enough outputs to fill the device.
 template <int Op>
 __global__ __launch_bounds__(kBlock) void cols_kernel(const float* __restrict__ x, float* __restrict__ out, int64_t outer,
                                                       int64_t len, int64_t inner) {
@@ -137,57 +133,94 @@ __global__ __launch_bounds__(kBlock) void cols_kernel(const float* __restrict__ 
     }
 }
 
-// Split columns: the axis is cut into `segs` equal segments; stage one writes a
-// partial per (segment, output) and stage two combines them in segment order.
-// Vec: four adjacent outputs per thread (inner % 4 == 0, aligned input).
+// ---- tiled column sums (few outputs, long axis: bias gradients) -------------------
+// Block (chunk, outer o, segment s): 16 column lanes x 16 row lanes. Column
+// lane c owns 4 adjacent columns (Vec) or 1; row lane r walks rows
+// a0 + r, a0 + r + 16, ... of the segment. Row lanes are then summed through
+// LDS in a fixed tree and one partial per (segment, column) is written.
+constexpr int kColLanes = 16, kRowLanes = 16;
+
 template <bool Vec>
-__global__ __launch_bounds__(kBlock) void cols_sum_partial_kernel(const float* __restrict__ x, double* __restrict__ part,
-                                                                  int64_t outer, int64_t len, int64_t inner, int64_t seg_len) {
-    const int64_t width = Vec ? inner / 4 : inner;
-    const int64_t items = outer * width;
-    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(kBlock) void colsum_tile_kernel(const float* __restrict__ x, double* __restrict__ part,
+                                                             int64_t outer, int64_t len, int64_t inner, int64_t seg_len,
+                                                             int64_t chunks) {
+    constexpr int W = Vec ? 4 : 1;
+    __shared__ double lds[kRowLanes][kColLanes * W + 1];
+    const int c = threadIdx.x % kColLanes, rl = threadIdx.x / kColLanes;
+    const int64_t chunk = blockIdx.x % chunks, o = blockIdx.x / chunks;
     const int64_t s = blockIdx.y;
-    if (t >= items) return;
-    const int64_t o = t / width, c = t % width;
+    const int64_t col = (chunk * kColLanes + c) * W;
     const int64_t a0 = s * seg_len, a1 = std::min(len, a0 + seg_len);
-    if (Vec) {
-        const float* base = x + o * len * inner + c * 4;
-        double s0 = 0, s1 = 0, s2 = 0, s3 = 0;
-        int64_t a = a0;
-        for (; a + 4 <= a1; a += 4) {  // four rows in flight per thread
-            const f4 v0 = ld4(base + a * inner), v1 = ld4(base + (a + 1) * inner), v2 = ld4(base + (a + 2) * inner),
-                     v3 = ld4(base + (a + 3) * inner);
-            s0 += double(v0.x); s1 += double(v0.y); s2 += double(v0.z); s3 += double(v0.w);
-            s0 += double(v1.x); s1 += double(v1.y); s2 += double(v1.z); s3 += double(v1.w);
-            s0 += double(v2.x); s1 += double(v2.y); s2 += double(v2.z); s3 += double(v2.w);
-            s0 += double(v3.x); s1 += double(v3.y); s2 += double(v3.z); s3 += double(v3.w);
+    double acc[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) acc[w] = 0.0;
+    if (col < inner) {
+        const float* base = x + o * len * inner + col;
+        int64_t a = a0 + rl;
+        for (; a + 3 * kRowLanes < a1; a += 4 * kRowLanes) {  // four rows in flight
+            if (Vec) {
+                const f4 v0 = ld4(base + a * inner), v1 = ld4(base + (a + kRowLanes) * inner),
+                         v2 = ld4(base + (a + 2 * kRowLanes) * inner), v3 = ld4(base + (a + 3 * kRowLanes) * inner);
+                acc[0] += double(v0.x); acc[1] += double(v0.y); acc[2] += double(v0.z); acc[3] += double(v0.w);
+                acc[0] += double(v1.x); acc[1] += double(v1.y); acc[2] += double(v1.z); acc[3] += double(v1.w);
+                acc[0] += double(v2.x); acc[1] += double(v2.y); acc[2] += double(v2.z); acc[3] += double(v2.w);
+                acc[0] += double(v3.x); acc[1] += double(v3.y); acc[2] += double(v3.z); acc[3] += double(v3.w);
+            } else {
+                const float v0 = base[a * inner], v1 = base[(a + kRowLanes) * inner],
+                            v2 = base[(a + 2 * kRowLanes) * inner], v3 = base[(a + 3 * kRowLanes) * inner];
+                acc[0] += double(v0);
+                acc[0] += double(v1);
+                acc[0] += double(v2);
+                acc[0] += double(v3);
+            }
         }
-        for (; a < a1; ++a) {
-            const f4 v = ld4(base + a * inner);
-            s0 += double(v.x); s1 += double(v.y); s2 += double(v.z); s3 += double(v.w);
+        for (; a < a1; a += kRowLanes) {
+            if (Vec) {
+                const f4 v = ld4(base + a * inner);
+                acc[0] += double(v.x); acc[1] += double(v.y); acc[2] += double(v.z); acc[3] += double(v.w);
+            } else {
+                acc[0] += double(base[a * inner]);
+            }
         }
-        double* p = part + s * outer * inner + o * inner + c * 4;
-        p[0] = s0;
-        p[1] = s1;
-        p[2] = s2;
-        p[3] = s3;
-    } else {
-        const float* base = x + o * len * inner + c;
-        double acc = 0.0;
-        for (int64_t a = a0; a < a1; ++a) acc += double(base[a * inner]);
-        part[s * outer * inner + o * inner + c] = acc;
+    }
+#pragma unroll
+    for (int w = 0; w < W; ++w) lds[rl][c * W + w] = acc[w];
+    __syncthreads();
+    // Fixed tree over the 16 row lanes: 8, 4, 2, 1.
+    for (int half = kRowLanes / 2; half > 0; half >>= 1) {
+        if (rl < half) {
+#pragma unroll
+            for (int w = 0; w < W; ++w) lds[rl][c * W + w] += lds[rl + half][c * W + w];
+        }
+        __syncthreads();
+    }
+    if (rl == 0) {
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+            if (col + w < inner) part[(s * outer + o) * inner + col + w] = lds[0][c * W + w];
     }
 }
 
-__global__ __launch_bounds__(kBlock) void cols_sum_combine_kernel(const double* __restrict__ part, float* __restrict__ out,
-                                                                  int64_t total, int64_t segs) {
+// out[t] = float(sum over segments of part[s][t]), in segment order. Loads are
+// issued eight at a time so a thread is not bound by one load's latency.
+__global__ __launch_bounds__(kBlock) void colsum_combine_kernel(const double* __restrict__ part, float* __restrict__ out,
+                                                                int64_t total, int64_t segs) {
     const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (t >= total) return;
     double acc = 0.0;
-    for (int64_t s = 0; s < segs; ++s) acc += part[s * total + t];
+    int64_t s = 0;
+    for (; s + 8 <= segs; s += 8) {
+        double v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = part[(s + k) * total + t];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc += v[k];
+    }
+    for (; s < segs; ++s) acc += part[s * total + t];
     out[t] = float(acc);
 }
 
+// ---- split columns for max/argmax --------------------------------------------------
 __global__ __launch_bounds__(kBlock) void cols_best_partial_kernel(const float* __restrict__ x, float* __restrict__ pv,
                                                                    int* __restrict__ pi, int64_t outer, int64_t len,
                                                                    int64_t inner, int64_t seg_len) {
@@ -217,50 +250,6 @@ __global__ __launch_bounds__(kBlock) void cols_best_combine_kernel(const float* 
     const float first = x[o * len * inner + i];
     if (first != first) b = Best{first, 0};
     out[t] = Op == 1 ? b.v : float(b.i);
-}
-
-// ---- full sum: fixed blocks of `chunk` elements, then one block ------------------
-__device__ inline double block_sum(double v, double* lds) {
-    v = wave_sum(v);
-    const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
-    if (lane == 0) lds[w] = v;
-    __syncthreads();
-    double total = 0.0;
-    if (threadIdx.x == 0)
-        for (int k = 0; k < int(blockDim.x / kWave); ++k) total += lds[k];
-    return total;  // valid in thread 0
-}
-
-template <bool Vec>
-__global__ __launch_bounds__(kBlock) void sum_partial_kernel(const float* __restrict__ x, double* __restrict__ part,
-                                                             int64_t n, int64_t chunk) {
-    __shared__ double lds[kBlock / kWave];
-    const int64_t b0 = int64_t(blockIdx.x) * chunk, b1 = std::min(n, b0 + chunk);
-    double acc = 0.0;
-    if (Vec) {  // b0 is a multiple of 4 (chunk is)
-        const int64_t v1 = b0 + (b1 - b0) / 4 * 4;
-        for (int64_t a = b0 + int64_t(threadIdx.x) * 4; a < v1; a += int64_t(blockDim.x) * 4) {
-            const f4 v = ld4(x + a);
-            acc += double(v.x);
-            acc += double(v.y);
-            acc += double(v.z);
-            acc += double(v.w);
-        }
-        for (int64_t a = v1 + threadIdx.x; a < b1; a += blockDim.x) acc += double(x[a]);
-    } else {
-        for (int64_t a = b0 + threadIdx.x; a < b1; a += blockDim.x) acc += double(x[a]);
-    }
-    const double total = block_sum(acc, lds);
-    if (threadIdx.x == 0) part[blockIdx.x] = total;
-}
-
-__global__ __launch_bounds__(kBlock) void sum_final_kernel(const double* __restrict__ part, float* __restrict__ out,
-                                                           int64_t blocks) {
-    __shared__ double lds[kBlock / kWave];
-    double acc = 0.0;
-    for (int64_t b = threadIdx.x; b < blocks; b += blockDim.x) acc += part[b];
-    const double total = block_sum(acc, lds);
-    if (threadIdx.x == 0) out[0] = float(total);
 }
 
 // ---- scatter_axis ---------------------------------------------------------------
@@ -306,6 +295,33 @@ void check_i32(int64_t v, const char* what) {
     if (v > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, std::string(what) + " exceeds the int32 index range");
 }
 
+void column_sum(Device& d, const float* in, float* out, int64_t outer, int64_t len, int64_t inner, const char* label) {
+    const bool vec = inner % 4 == 0 && aligned16(in);
+    const int64_t width = vec ? 4 * kColLanes : kColLanes;
+    const int64_t chunks = (inner + width - 1) / width;
+    const int64_t blocks_x = outer * chunks;
+    // Segments: a function of the shape only; aim at ~2048 workgroups, at
+    // least 64 rows per segment, at most 64 segments.
+    int64_t segs = std::max<int64_t>(1, (2048 + blocks_x - 1) / blocks_x);
+    segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / 64), 64});
+    const int64_t seg_len = (len + segs - 1) / segs;
+    segs = (len + seg_len - 1) / seg_len;
+    if (blocks_x > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, "reduction too large");
+    const int64_t total = outer * inner;
+    Scratch part(size_t(segs * total) * sizeof(double));
+    const dim3 grid(static_cast<unsigned>(blocks_x), static_cast<unsigned>(segs));
+    if (vec)
+        hipLaunchKernelGGL(colsum_tile_kernel<true>, grid, dim3(kBlock), 0, d.stream, in, part.as<double>(), outer, len,
+                           inner, seg_len, chunks);
+    else
+        hipLaunchKernelGGL(colsum_tile_kernel<false>, grid, dim3(kBlock), 0, d.stream, in, part.as<double>(), outer, len,
+                           inner, seg_len, chunks);
+    after_launch(label);
+    hipLaunchKernelGGL(colsum_combine_kernel, dim3(unsigned((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, d.stream,
+                       part.as<double>(), out, total, segs);
+    after_launch(label);
+}
+
 }  // namespace
 }  // namespace vchip
 
@@ -318,24 +334,21 @@ int vc_hip_reduce_sum(const float* in, size_t count, float* out) {
         Device& d = require_device();
         if (!out) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_reduce_sum: null output");
         const int64_t n = int64_t(count);
-        // Partition fixed by n: chunks of at least 8192 elements, at most 2048 chunks.
-        int64_t chunk = std::max<int64_t>(8192, (n + 2047) / 2048);
-        chunk = (chunk + 1023) / 1024 * 1024;
-        const int64_t blocks = n == 0 ? 1 : (n + chunk - 1) / chunk;
-        Scratch part(size_t(blocks) * sizeof(double));
+        const int64_t chunk = red::sum_chunk(n);
+        const int64_t blocks = n == 0 ? 0 : (n + chunk - 1) / chunk;
+        Scratch part(size_t(std::max<int64_t>(blocks, 1)) * sizeof(double));
         Profiled p("reduce_sum", double(n), 4.0 * double(n));
-        if (n == 0) {
-            hipLaunchKernelGGL(sum_final_kernel, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), out, int64_t(0));
-        } else {
+        if (blocks > 0) {
             if (aligned16(in))
-                hipLaunchKernelGGL(sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, in,
+                hipLaunchKernelGGL(red::sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, in,
                                    part.as<double>(), n, chunk);
             else
-                hipLaunchKernelGGL(sum_partial_kernel<false>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, in,
+                hipLaunchKernelGGL(red::sum_partial_kernel<false>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, in,
                                    part.as<double>(), n, chunk);
             after_launch("reduce_sum");
-            hipLaunchKernelGGL(sum_final_kernel, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), out, blocks);
         }
+        hipLaunchKernelGGL(red::sum_final_kernel<red::Identity>, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), out,
+                           blocks, red::Identity());
         after_launch("reduce_sum");
         p.done();
     });
@@ -350,17 +363,17 @@ int vc_hip_reduce_axis(const float* in, float* out, size_t outer_, size_t length
         const int64_t outer = int64_t(outer_), len = int64_t(length_), inner = int64_t(inner_);
         const int64_t total = outer * inner;
         if (total == 0) return;
+        const char* label = op == VC_REDUCE_SUM ? "reduce_axis_sum" : op == VC_REDUCE_MAX ? "reduce_axis_max" : "reduce_axis_argmax";
         if (len == 0) {  // sum over an empty axis is zero
             hipLaunchKernelGGL(zero_kernel, dim3(grid_1d(size_t(total), kBlock, 1024)), dim3(kBlock), 0, d.stream, out, total);
-            after_launch("reduce_axis_sum");
+            after_launch(label);
             return;
         }
         check_i32(len, "reduction axis length");
-        const char* label = op == VC_REDUCE_SUM ? "reduce_axis_sum" : op == VC_REDUCE_MAX ? "reduce_axis_max" : "reduce_axis_argmax";
         Profiled p(label, double(outer * len * inner), 4.0 * double(outer * len * inner + total));
         const int64_t target_threads = int64_t(d.cu_count) * 1024;
         if (inner == 1) {
-            // One wavefront per row; rows of < 16 elements waste lanes but stay correct.
+            // One wavefront per row; rows of < 64 elements leave lanes idle but stay correct.
             const bool vec = len % 4 == 0 && aligned16(in);
             const unsigned grid = unsigned(std::min<int64_t>((outer + 3) / 4, int64_t(d.cu_count) * 64));
 #define VC_ROWS(OP)                                                                                              \
@@ -374,9 +387,7 @@ int vc_hip_reduce_axis(const float* in, float* out, size_t outer_, size_t length
             p.done();
             return;
         }
-        const bool vec = op == VC_REDUCE_SUM && inner % 4 == 0 && aligned16(in);
-        const int64_t items = vec ? total / 4 : total;
-        if (items >= target_threads || len < 32) {
+        if (total >= target_threads || len < 64) {
             const unsigned grid = grid_1d(size_t(total), kBlock, unsigned(d.cu_count) * 64);
             if (op == VC_REDUCE_SUM) hipLaunchKernelGGL(cols_kernel<0>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
             else if (op == VC_REDUCE_MAX) hipLaunchKernelGGL(cols_kernel<1>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
@@ -385,36 +396,28 @@ int vc_hip_reduce_axis(const float* in, float* out, size_t outer_, size_t length
             p.done();
             return;
         }
-        // Split the axis so that items * segs covers the device; segments of >= 16 rows.
-        int64_t segs = std::min<int64_t>((target_threads + items - 1) / items, (len + 15) / 16);
+        if (op == VC_REDUCE_SUM) {
+            column_sum(d, in, out, outer, len, inner, label);
+            p.done();
+            return;
+        }
+        // max/argmax with few outputs: split the axis into segments of >= 16 rows.
+        int64_t segs = std::min<int64_t>((target_threads + total - 1) / total, (len + 15) / 16);
         segs = std::max<int64_t>(1, std::min<int64_t>(segs, 1024));
         const int64_t seg_len = (len + segs - 1) / segs;
         segs = (len + seg_len - 1) / seg_len;
-        const dim3 grid1(unsigned((items + kBlock - 1) / kBlock), unsigned(segs));
+        const dim3 grid1(unsigned((total + kBlock - 1) / kBlock), unsigned(segs));
         const unsigned grid2 = unsigned((total + kBlock - 1) / kBlock);
-        if (op == VC_REDUCE_SUM) {
-            Scratch part(size_t(segs * total) * sizeof(double));
-            if (vec)
-                hipLaunchKernelGGL(cols_sum_partial_kernel<true>, grid1, dim3(kBlock), 0, d.stream, in, part.as<double>(), outer,
-                                   len, inner, seg_len);
-            else
-                hipLaunchKernelGGL(cols_sum_partial_kernel<false>, grid1, dim3(kBlock), 0, d.stream, in, part.as<double>(),
-                                   outer, len, inner, seg_len);
-            after_launch(label);
-            hipLaunchKernelGGL(cols_sum_combine_kernel, dim3(grid2), dim3(kBlock), 0, d.stream, part.as<double>(), out, total,
-                               segs);
-        } else {
-            Scratch pv(size_t(segs * total) * sizeof(float)), pi(size_t(segs * total) * sizeof(int));
-            hipLaunchKernelGGL(cols_best_partial_kernel, grid1, dim3(kBlock), 0, d.stream, in, pv.as<float>(), pi.as<int>(),
-                               outer, len, inner, seg_len);
-            after_launch(label);
-            if (op == VC_REDUCE_MAX)
-                hipLaunchKernelGGL(cols_best_combine_kernel<1>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv.as<float>(),
-                                   pi.as<int>(), out, outer, len, inner, segs);
-            else
-                hipLaunchKernelGGL(cols_best_combine_kernel<2>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv.as<float>(),
-                                   pi.as<int>(), out, outer, len, inner, segs);
-        }
+        Scratch pv(size_t(segs * total) * sizeof(float)), pi(size_t(segs * total) * sizeof(int));
+        hipLaunchKernelGGL(cols_best_partial_kernel, grid1, dim3(kBlock), 0, d.stream, in, pv.as<float>(), pi.as<int>(), outer,
+                           len, inner, seg_len);
+        after_launch(label);
+        if (op == VC_REDUCE_MAX)
+            hipLaunchKernelGGL(cols_best_combine_kernel<1>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv.as<float>(),
+                               pi.as<int>(), out, outer, len, inner, segs);
+        else
+            hipLaunchKernelGGL(cols_best_combine_kernel<2>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv.as<float>(),
+                               pi.as<int>(), out, outer, len, inner, segs);
         after_launch(label);
         p.done();
     });
@@ -437,9 +440,9 @@ int vc_hip_transpose_last2(const float* in, float* out, size_t batch, size_t row
     return guard([&] {
         Device& d = require_device();
         if (batch * rows * cols == 0) return;
+        if ((rows + kTile - 1) / kTile > 65535) fail(VC_HIP_ERR_OVERFLOW, "transpose: too many rows");
         const dim3 grid(unsigned((cols + kTile - 1) / kTile), unsigned((rows + kTile - 1) / kTile),
                         unsigned(std::min<size_t>(batch, 65535)));
-        if ((rows + kTile - 1) / kTile > 65535) fail(VC_HIP_ERR_OVERFLOW, "transpose: too many rows");
         Profiled p("transpose_last2", 0.0, 8.0 * double(batch * rows * cols));
         hipLaunchKernelGGL(transpose_kernel, grid, dim3(kTile, 8), 0, d.stream, in, out, int64_t(batch), int64_t(rows),
                            int64_t(cols));

@@ -14,6 +14,7 @@
 //
 // The reference's masked sum also turns any non-finite non-target log-prob
 // into NaN (inf * 0); the forward reproduces that.
+#include "reduce_common.hpp"
 #include "vc_hip_internal.hpp"
 
 #include <algorithm>
@@ -116,23 +117,15 @@ __global__ __launch_bounds__(kBlock) void xent_rows_kernel(const float* __restri
     }
 }
 
-// loss = -(float)(sum terms) / (float)rows, the sum in double over a fixed tree.
-__global__ __launch_bounds__(kBlock) void xent_loss_kernel(const float* __restrict__ terms, int64_t rows,
-                                                           float* __restrict__ loss) {
-    __shared__ double lds[kBlock / kWave];
-    double acc = 0.0;
-    for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) acc += double(terms[r]);
-    for (int off = kWave / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
-    if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double total = 0.0;
-        for (int w = 0; w < int(blockDim.x / kWave); ++w) total += lds[w];
-        const float sum = float(total);
+// loss = -(float)(sum of row terms) / (float)rows: negate, then divide, as
+// -(...).sum() / batch evaluates (src/nn.cpp:52).
+struct NegateDivide {
+    float rows;
+    __device__ float operator()(float sum) const {
         const float negated = -sum;
-        loss[0] = negated / float(rows);
+        return negated / rows;
     }
-}
+};
 
 template <bool Vec>
 __global__ __launch_bounds__(kBlock) void xent_backward_kernel(const float* __restrict__ x, const int* __restrict__ targets,
@@ -190,7 +183,15 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
             hipLaunchKernelGGL(xent_rows_kernel<false>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, R, C,
                                row_stats, terms.as<float>());
         after_launch("xent_forward");
-        hipLaunchKernelGGL(xent_loss_kernel, dim3(1), dim3(kBlock), 0, d.stream, terms.as<float>(), R, loss);
+        // Row terms -> loss with the shared deterministic two-stage sum.
+        const int64_t chunk = red::sum_chunk(R);
+        const int64_t blocks = (R + chunk - 1) / chunk;
+        Scratch part(size_t(blocks) * sizeof(double));
+        hipLaunchKernelGGL(red::sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream,
+                           terms.as<float>(), part.as<double>(), R, chunk);
+        after_launch("xent_forward");
+        hipLaunchKernelGGL(red::sum_final_kernel<NegateDivide>, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), loss,
+                           blocks, NegateDivide{float(R)});
         after_launch("xent_forward");
         p.done();
     });

@@ -38,7 +38,7 @@ def log(*args):
     print(*args, file=sys.stderr, flush=True)
 
 
-def gpu_bench(steps: int, warmup: int):
+def gpu_bench(steps: int, warmup: int, copy_calibration: bool = False):
     import numpy as np
 
     import vectorcore_amd as vc
@@ -66,6 +66,14 @@ def gpu_bench(steps: int, warmup: int):
         vc.zero_grad(params)
         return loss.item()
 
+    if copy_calibration:
+        # A plain streaming pass of known size (read 256 MiB, write 256 MiB)
+        # whose FETCH_SIZE/WRITE_SIZE counters calibrate the traffic readings.
+        src = vc.Tensor.zeros([64 << 20], device="hip")
+        for _ in range(3):
+            _ = -src
+        vc.synchronize()
+        del src, _
     losses = [step() for _ in range(warmup)]
     allocs_before = vc.hip_pool_stats()["device_allocations"]
     vc.synchronize()
@@ -139,13 +147,15 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first stream 256 MiB through a negate kernel (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the data-parallel "
               "sharding of this workload is a design note, not a launched path)", file=sys.stderr)
         sys.exit(2)
 
-    r = gpu_bench(args.steps, args.warmup)
+    r = gpu_bench(args.steps, args.warmup, args.copy_calibration)
     prof = r["prof"]
     ms_per_step = r["elapsed"] * 1e3 / args.steps
     bwd = [v for k, v in prof.items() if k in ("gemm_nt", "gemm_tn")]

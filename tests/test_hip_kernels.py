@@ -74,6 +74,22 @@ def test_gemm_batched_offsets_affine_and_table():
         np.testing.assert_allclose(got[z], K.matmul2d(a[z], b[0]), rtol=1e-4, atol=1e-4 * np.sqrt(k))
 
 
+def test_gemm_split_k_long_reductions():
+    """Few output tiles and a long K: the K range is split across workgroups
+    and the partial products are summed in split order, so results repeat
+    bit for bit."""
+    rng = np.random.default_rng(11)
+    for (m, k, n, batch) in ((257, 4133, 383, 1), (64, 2100, 96, 3), (130, 8192, 1, 1)):
+        for ta, tb in ((0, 0), (1, 0), (0, 1), (1, 1)):
+            a = rng.uniform(-1, 1, size=(batch,) + ((k, m) if ta else (m, k))).astype(np.float32)
+            b = rng.uniform(-1, 1, size=(batch,) + ((n, k) if tb else (k, n))).astype(np.float32)
+            got = run_gemm(a, b, m, k, n, ta, tb, batch=batch)
+            for z in range(batch):
+                np.testing.assert_allclose(got[z], K.matmul2d(a[z], b[z], bool(ta), bool(tb)), rtol=1e-4,
+                                           atol=1e-4 * np.sqrt(k), err_msg=f"{m}x{k}x{n} b{batch} ta={ta} tb={tb}")
+            np.testing.assert_array_equal(run_gemm(a, b, m, k, n, ta, tb, batch=batch), got)
+
+
 def test_gemm_batch_reduce_matches_summed_products():
     """dB of a batch-broadcast B: sum_z A[z]^T dC[z] in one launch."""
     bm = W.bmm(batch=3, m=96, k=80, n=72, seed=1)

@@ -10,9 +10,10 @@
 // four waves owns a 64 x 64 quadrant as 2 x 2 blocks of
 // V_MFMA_F32_32X32X2_F32 (A: lane l holds A[l%32][k], B: B[k][l%32], k = l/32;
 // D: 16 values per lane, row 8(v/4) + 4(l/32) + v%4, column l%32 — checked on
-// the device). K advances in slices of 32: while the waves run the 64 MFMAs of
-// one slice from LDS, every thread already holds the next slice's global loads
-// in registers.
+// the device). K advances in slices of 32 through two LDS stages with one
+// barrier per slice (the pipeline is described at gemm_mfma_kernel). Outputs
+// with few tiles and a long K split K into ranges whose partial products are
+// summed in range order by a second pass.
 //
 // LDS layout follows each operand's contiguous axis, so no transposing stores:
 //  - k-contiguous operand (A in NN/NT, B in NT): [128][32 + 4] floats; a lane
@@ -62,6 +63,8 @@ struct GemmArgs {
     int64_t reduce;                // products summed into each output
     int64_t a_rstride, b_rstride;
     int tiles_m, tiles_n;
+    int splits;                    // K split into this many ranges (partials summed afterwards)
+    int kt_per_split;              // BK slices per split
 };
 
 // Tile id -> (tile_m, tile_n) with the XCD remap and grouped order.
@@ -81,6 +84,12 @@ __device__ inline void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, i
     tn = local / group_rows;
 }
 
+__device__ inline int64_t uniform64(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(uint64_t(v)));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(uint64_t(v) >> 32));
+    return int64_t((uint64_t(hi) << 32) | lo);
+}
+
 // Buffer resource over `base` (gfx9 descriptor word 3). Offsets at or above
 // kOutOfRange fall outside num_records: loads return 0, stores are dropped.
 // The raw buffer builtins move 32-bit integers; values are bit-cast.
@@ -89,108 +98,107 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), short(0), int(kOutOfRange - 1), 0x00020000);
 }
 
-// Global -> register loader for one operand tile (128 along m/n, BK along k).
-// The tile origin is uniform (scalar registers); each thread keeps 32-bit byte
-// offsets of its four 16-byte slots, their k position and whether their m/n
-// row is inside the matrix. Edges are masked by pointing a slot out of range.
+// Global -> register loader for one operand tile (128 along m/n, BK along k),
+// in four 16-byte slots per thread. Slot q of a k-contiguous operand is row
+// mn0 + 32 q, k k0 (8 threads per 32-float row); slot q of an m/n-contiguous
+// operand is k-row k0 + 8 q, column mn0 (32 threads per 128-float row). Each
+// thread keeps one byte offset (slot 0); slots step by a uniform amount passed
+// as the instruction's scalar offset. The tile origin is uniform (scalar
+// registers). Edges are masked by pointing a slot out of range.
 // KC: operand contiguous along k.
 template <bool KC, bool Vec>
 struct TileLoader {
     const float* origin;  // element (mn0, 0) of this operand
     int64_t step;         // elements per BK slice
-    int K;
-    uint32_t boff[4];
-    int kpos[4];
-    int mn_ok;
-    int ld, mn_lim;       // scalar path: row stride, rows left in the matrix
+    int K, mn_lim;        // k extent; rows/columns left in the matrix from the tile origin
+    uint32_t qstep;       // bytes between slots
+    uint32_t ld4;         // bytes per stored row
+    uint32_t voff;        // this thread's byte offset of slot 0 within a slice
+    int mn0, k0;          // this thread's slot-0 coordinates within the tile
 
-    __device__ void init(const float* base, int ld_, int mn0, int MN, int K_) {
+    __device__ void init(const float* base, int ld, int mn_origin, int MN, int K_) {
         K = K_;
-        ld = ld_;
-        mn_lim = MN - mn0;
-        origin = KC ? base + int64_t(mn0) * ld : base + mn0;
+        mn_lim = MN - mn_origin;
+        origin = KC ? base + int64_t(mn_origin) * ld : base + mn_origin;
         step = KC ? int64_t(BK) : int64_t(BK) * ld;
-        mn_ok = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int idx = threadIdx.x + q * kThreads;
-            int mn_local, k_local;
-            if (KC) {  // 128 rows x 8 vectors along k
-                mn_local = idx / (BK / 4);
-                k_local = (idx % (BK / 4)) * 4;
-                boff[q] = uint32_t(mn_local * ld + k_local) * 4u;
-            } else {  // 32 k-rows x 32 vectors along m/n
-                k_local = idx / (BM / 4);
-                mn_local = (idx % (BM / 4)) * 4;
-                boff[q] = uint32_t(k_local * ld + mn_local) * 4u;
-            }
-            if (mn_local < mn_lim) mn_ok |= 1 << q;
-            kpos[q] = k_local;
+        ld4 = uint32_t(ld) * 4u;
+        const int t = threadIdx.x;
+        if (KC) {
+            mn0 = t / (BK / 4);
+            k0 = (t % (BK / 4)) * 4;
+            qstep = 32u * ld4;
+        } else {
+            k0 = t / (BM / 4);
+            mn0 = (t % (BM / 4)) * 4;
+            qstep = 8u * ld4;
         }
+        voff = KC ? uint32_t(mn0) * ld4 + uint32_t(k0) * 4u : uint32_t(k0) * ld4 + uint32_t(mn0) * 4u;
     }
 
-    __device__ void load(int kt, f4 (&reg)[4]) const {
-        const int k0 = kt * BK;
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(origin + int64_t(kt) * step);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if (Vec) {
-                const bool ok = ((mn_ok >> q) & 1) && (k0 + kpos[q] < K);
-                reg[q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? boff[q] : kOutOfRange, 0, 0));
-            } else {
-                const int idx = threadIdx.x + q * kThreads;
-                f4 v;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    int mn, k;
-                    if (KC) {
-                        mn = idx / (BK / 4);
-                        k = (idx % (BK / 4)) * 4 + e;
-                    } else {
-                        k = idx / (BM / 4);
-                        mn = (idx % (BM / 4)) * 4 + e;
-                    }
-                    const bool ok = mn < mn_lim && k0 + k < K;
-                    const uint32_t off = uint32_t(KC ? mn * ld + k : k * ld + mn) * 4u;
-                    v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? off : kOutOfRange, 0, 0));
-                }
-                reg[q] = v;
-            }
+    __device__ __amdgpu_buffer_rsrc_t slice(int kt) const { return make_rsrc(origin + int64_t(kt) * step); }
+
+    // Slot q of slice kt. Slices past K read as zeros without touching memory.
+    __device__ f4 load(__amdgpu_buffer_rsrc_t rs, int kt, int q) const {
+        const int k = kt * BK + k0 + (KC ? 0 : 8 * q);
+        const int mn = mn0 + (KC ? 32 * q : 0);
+        const uint32_t soff = uint32_t(q) * qstep;
+        if (Vec) {
+            const bool ok = mn < mn_lim && k < K;
+            return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? voff : kOutOfRange, soff, 0));
         }
+        f4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bool ok = KC ? (mn < mn_lim && k + e < K) : (mn + e < mn_lim && k < K);
+            v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? voff + 4u * e : kOutOfRange,
+                                                                                    soff, 0));
+        }
+        return v;
     }
+
+    // Byte offset of this thread's slot 0 in an LDS stage; slot q adds
+    // q * lds_qstep.
+    __device__ uint32_t lds_off() const {
+        return KC ? uint32_t(mn0 * (BK + kPadK) + k0) * 4u : uint32_t(k0 * (BM + kPadMN) + mn0) * 4u;
+    }
+    static constexpr uint32_t lds_qstep = KC ? 32u * (BK + kPadK) * 4u : 8u * (BM + kPadMN) * 4u;
 };
 
-template <bool KC>
-__device__ inline void store_slice(float* __restrict__ lds, const f4 (&reg)[4]) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int idx = threadIdx.x + q * kThreads;
-        if (KC) {
-            const int row = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
-            *reinterpret_cast<f4*>(lds + row * (BK + kPadK) + c) = reg[q];
-        } else {
-            const int row = idx / (BM / 4), c = (idx % (BM / 4)) * 4;
-            *reinterpret_cast<f4*>(lds + row * (BM + kPadMN) + c) = reg[q];
-        }
-    }
+// Slot q of a slice into an LDS stage (`off` from TileLoader::lds_off).
+template <bool KC, bool Vec>
+__device__ inline void store_slot(char* __restrict__ lds, uint32_t off, const f4& v, int q) {
+    *reinterpret_cast<f4*>(lds + off + q * TileLoader<KC, Vec>::lds_qstep) = v;
 }
 
-// Fragment values of 4 MFMA steps (k-group g) for the 32-row block at `off`.
+// Part s (0..3) of the fragments of k-group g for the wave's two 32-row
+// blocks at `off` and `off + 32`: frag[b][s'] is the value for MFMA step s'.
+// A k-contiguous operand reads block s's 4 values with one ds_read_b128 (at
+// parts `first` and `first + 1`); an m/n-contiguous operand reads step s of
+// both blocks.
 template <bool KC>
-__device__ inline f4 read_frag(const float* __restrict__ lds, int off, int g, int lane) {
+__device__ inline void read_part(const float* __restrict__ lds, int off, int g, int lane, int s, int first,
+                                 f4 (&frag)[2]) {
     const int r = off + (lane & 31);
     const int kb = g * 8 + 4 * (lane >> 5);
-    if (KC) return *reinterpret_cast<const f4*>(lds + r * (BK + kPadK) + kb);
-    f4 v;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) v[s] = lds[(kb + s) * (BM + kPadMN) + r];
-    return v;
+    if (KC) {
+        const int b = s - first;
+        if (b == 0 || b == 1) frag[b] = *reinterpret_cast<const f4*>(lds + (r + 32 * b) * (BK + kPadK) + kb);
+    } else {
+        frag[0][s] = lds[(kb + s) * (BM + kPadMN) + r];
+        frag[1][s] = lds[(kb + s) * (BM + kPadMN) + r + 32];
+    }
 }
 
 template <bool TA, bool TB, bool Vec>
 __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
-    __shared__ __attribute__((aligned(16))) float As[kLdsTile];
-    __shared__ __attribute__((aligned(16))) float Bs[kLdsTile];
+    // Two LDS stages. Step kt multiplies out of stage cur while its first k-group
+    // also stores slice kt + 1 (in registers since step kt - 1) into the other
+    // stage and issues the global loads of slice kt + 2. Fragments are read one
+    // k-group ahead; after the third group's MFMAs one barrier makes stage
+    // cur ^ 1 complete and stage cur free, and the fourth group's MFMAs overlap
+    // the reads of the next step's first group.
+    __shared__ __attribute__((aligned(16))) float As[2][kLdsTile];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kLdsTile];
     constexpr bool AKC = !TA;  // A contiguous along k
     constexpr bool BKC = TB;   // B contiguous along k
     int tm, tn;
@@ -199,17 +207,20 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-    const int kt_count = (p.K + BK - 1) / BK;
+    const int kt_total = (p.K + BK - 1) / BK;
+    const int64_t jobs = p.batch * p.splits;
 
-    for (int64_t z = blockIdx.y; z < p.batch; z += gridDim.y) {
-        int64_t aoff, boff;
-        if (p.table) {
-            aoff = p.table[2 * z];
-            boff = p.table[2 * z + 1];
-        } else {
-            aoff = z * p.a_bstride;
-            boff = z * p.b_bstride;
-        }
+    for (int64_t job = blockIdx.y; job < jobs; job += gridDim.y) {
+        // Per-job values are workgroup-uniform; saying so keeps the buffer
+        // descriptors in scalar registers (a 64-bit division or a table read
+        // would otherwise leave them in vector registers and every buffer
+        // access would become a per-lane loop).
+        const int64_t z = uniform64(job / p.splits);
+        const int split = __builtin_amdgcn_readfirstlane(int(job - z * p.splits));
+        const int kt_begin = split * p.kt_per_split;
+        const int kt_end = min(kt_total, kt_begin + p.kt_per_split);
+        const int64_t aoff = uniform64(p.table ? p.table[2 * z] : z * p.a_bstride);
+        const int64_t boff = uniform64(p.table ? p.table[2 * z + 1] : z * p.b_bstride);
         f16v acc[2][2];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -218,45 +229,86 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-        for (int64_t r = 0; r < p.reduce; ++r) {
+        for (int64_t r = 0; r < p.reduce && kt_begin < kt_end; ++r) {
             TileLoader<AKC, Vec> la;
             TileLoader<BKC, Vec> lb;
             la.init(p.a + aoff + r * p.a_rstride, p.lda, m0, p.M, p.K);
             lb.init(p.b + boff + r * p.b_rstride, p.ldb, n0, p.N, p.K);
             f4 ra[4], rb[4];
-            if (kt_count > 0) {
-                la.load(0, ra);
-                lb.load(0, rb);
-            }
-            for (int kt = 0; kt < kt_count; ++kt) {
-                __syncthreads();  // the previous slice is no longer read
-                store_slice<AKC>(As, ra);
-                store_slice<BKC>(Bs, rb);
-                __syncthreads();
-                if (kt + 1 < kt_count) {  // next slice in flight during the MFMAs
-                    la.load(kt + 1, ra);
-                    lb.load(kt + 1, rb);
+            char* const lds_a = reinterpret_cast<char*>(As[0]);
+            char* const lds_b = reinterpret_cast<char*>(Bs[0]);
+            const uint32_t a_st = la.lds_off(), b_st = lb.lds_off();
+            {
+                const __amdgpu_buffer_rsrc_t sa = la.slice(kt_begin), sb = lb.slice(kt_begin);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    store_slot<AKC, Vec>(lds_a, a_st, la.load(sa, kt_begin, q), q);
+                    store_slot<BKC, Vec>(lds_b, b_st, lb.load(sb, kt_begin, q), q);
                 }
+                const __amdgpu_buffer_rsrc_t na = la.slice(kt_begin + 1), nb = lb.slice(kt_begin + 1);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    ra[q] = la.load(na, kt_begin + 1, q);
+                    rb[q] = lb.load(nb, kt_begin + 1, q);
+                }
+            }
+            __syncthreads();
+            f4 fa[2][2], fb[2][2];  // [k-group parity][32-row block]
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                read_part<AKC>(As[0], wm, 0, lane, s, 0, fa[0]);
+                read_part<BKC>(Bs[0], wn, 0, lane, s, 2, fb[0]);
+            }
+            for (int kt = kt_begin; kt < kt_end; ++kt) {
+                const int cur = (kt - kt_begin) & 1;
+                const float* as = As[cur];
+                const float* bs = Bs[cur];
+                float* as_next = As[cur ^ 1];
+                float* bs_next = Bs[cur ^ 1];
+                char* const st_a = lds_a + (cur ^ 1) * kLdsTile * 4;
+                char* const st_b = lds_b + (cur ^ 1) * kLdsTile * 4;
+                // Past the end of the range the stores and loads below are idle
+                // work (slices past K are masked), kept so each step is straight-line.
+                const __amdgpu_buffer_rsrc_t sa = la.slice(kt + 2), sb = lb.slice(kt + 2);
 #pragma unroll
                 for (int g = 0; g < BK / 8; ++g) {
-                    f4 fa[2], fb[2];
+                    const int cb = g & 1;
+                    if (g == BK / 8 - 1) __syncthreads();
 #pragma unroll
-                    for (int i = 0; i < 2; ++i) fa[i] = read_frag<AKC>(As, wm + 32 * i, g, lane);
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) fb[j] = read_frag<BKC>(Bs, wn + 32 * j, g, lane);
-#pragma unroll
-                    for (int s = 0; s < 4; ++s)
+                    for (int s = 0; s < 4; ++s) {
+                        if (g == 0) {
+                            store_slot<AKC, Vec>(st_a, a_st, ra[s], s);
+                            store_slot<BKC, Vec>(st_b, b_st, rb[s], s);
+                            ra[s] = la.load(sa, kt + 2, s);
+                            rb[s] = lb.load(sb, kt + 2, s);
+                        }
+                        if (g + 1 < BK / 8) {
+                            read_part<AKC>(as, wm, g + 1, lane, s, 0, fa[cb ^ 1]);
+                            read_part<BKC>(bs, wn, g + 1, lane, s, 2, fb[cb ^ 1]);
+                        } else {
+                            read_part<AKC>(as_next, wm, 0, lane, s, 0, fa[cb ^ 1]);
+                            read_part<BKC>(bs_next, wn, 0, lane, s, 2, fb[cb ^ 1]);
+                        }
 #pragma unroll
                         for (int i = 0; i < 2; ++i)
 #pragma unroll
                             for (int j = 0; j < 2; ++j)
-                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[cb][i][s], fb[cb][j][s], acc[i][j],
+                                                                                 0, 0, 0);
+                        // Keep this order: the scheduler would otherwise sink
+                        // each LDS read to just before its first use.
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
             }
+            // The last step's look-ahead reads touched the other stage.
+            __syncthreads();
         }
         // Epilogue: buffer stores relative to the tile origin; rows/columns
-        // outside C are pointed out of range and dropped by the hardware.
-        const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.c + z * int64_t(p.M) * p.N + int64_t(m0) * p.N + n0);
+        // outside C are pointed out of range and dropped by the hardware. With a
+        // split K each split writes its own partial matrix.
+        float* C = p.c + (p.splits > 1 ? job : z) * int64_t(p.M) * p.N;
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(C + int64_t(m0) * p.N + n0);
         const int row_lim = p.M - m0, col_lim = p.N - n0;
         const int row0 = wm + 4 * (lane >> 5);
 #pragma unroll
@@ -274,6 +326,20 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
                                                           0, 0);
                 }
             }
+    }
+}
+
+// Split-K combine: c[z][i] = sum over s of part[z][s][i], in split order.
+__global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ part, float* __restrict__ c,
+                                                        int64_t batch, int64_t mn, int splits) {
+    const int64_t total = batch * mn;
+    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+        const int64_t z = t / mn, i = t % mn;
+        const float* src = part + z * splits * mn + i;
+        float acc = src[0];
+        for (int s = 1; s < splits; ++s) acc += src[int64_t(s) * mn];
+        c[t] = acc;
     }
 }
 
@@ -372,7 +438,20 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     } else {
         vec = vec && a_bstride % 4 == 0 && b_bstride % 4 == 0;
     }
-    const dim3 grid(unsigned(tiles), unsigned(std::min<int64_t>(batch, 65535)));
+    // Split K when the output has fewer tiles than two workgroups per CU and
+    // K is long: each split accumulates its K range into a partial matrix and
+    // a second pass sums the partials in split order (deterministic).
+    const int kt_total = int((K + BK - 1) / BK);
+    int splits = 1;
+    if (!simple && reduce == 1 && tiles * batch < 2 * int64_t(d.cu_count) && kt_total >= 64) {
+        splits = int(std::min<int64_t>((2 * int64_t(d.cu_count) + tiles * batch - 1) / (tiles * batch), 4));
+        splits = std::min(splits, kt_total / 32);
+    }
+    args.splits = splits;
+    args.kt_per_split = (kt_total + splits - 1) / splits;
+    Scratch partials(splits > 1 ? size_t(batch * splits) * size_t(M * N) * sizeof(float) : 4);
+    if (splits > 1) args.c = partials.as<float>();
+    const dim3 grid(unsigned(tiles), unsigned(std::min<int64_t>(batch * splits, 65535)));
     const char* label = variant_label(ta, tb);
     const double flops = 2.0 * double(M) * double(N) * double(K) * double(batch) * double(reduce);
     const double bytes = 4.0 * (double(M * K + K * N) * double(reduce) + double(M * N)) * double(batch);
@@ -381,6 +460,12 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     else if (ta) launch_variant<true, false>(args, vec, simple, grid, d.stream);
     else if (tb) launch_variant<false, true>(args, vec, simple, grid, d.stream);
     else launch_variant<false, false>(args, vec, simple, grid, d.stream);
+    if (splits > 1) {
+        after_launch(label);
+        const int64_t total = batch * M * N;
+        hipLaunchKernelGGL(split_sum_kernel, dim3(unsigned(std::min<int64_t>((total + 255) / 256, int64_t(d.cu_count) * 16))),
+                           dim3(256), 0, d.stream, partials.as<float>(), c, batch, M * N, splits);
+    }
     after_launch(label);
     prof.done();
 }

@@ -27,13 +27,11 @@ using red::kBlock;
 using red::kWave;
 using red::ld4;
 
-constexpr int kNone = std::numeric_limits<int>::max();  // "no candidate yet"
+using red::Best;
+using red::kNone;
 
-struct Best {
-    float v;
-    int i;
-};
-
+// Column paths visit a segment in order but merge segments by index, so they
+// keep the general rule: NaN skipped, larger value first, then smaller index.
 __device__ inline void consider(Best& b, float v, int i) {
     if (v != v) return;  // NaN never becomes the best after the first element
     if (b.i == kNone || v > b.v || (v == b.v && i < b.i)) {
@@ -48,32 +46,44 @@ __device__ inline Best combine(Best a, Best b) {
     return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
 }
 
-__device__ inline Best wave_best(Best b) {
-    for (int off = kWave / 2; off > 0; off >>= 1) {
-        Best o{__shfl_xor(b.v, off, kWave), __shfl_xor(b.i, off, kWave)};
-        b = combine(b, o);
-    }
-    return b;
-}
-
 // ---- rows: inner == 1, one wavefront per row -----------------------------------
-// Op: 0 sum, 1 max, 2 argmax.
-template <int Op, bool Vec>
+// Op: 0 sum, 1 max, 2 argmax. With NV > 0 (rows of at most 256 NV elements, a
+// multiple of 4) each lane loads its NV float4 at once before reducing;
+// otherwise it streams. Both visit a lane's elements in the same order.
+template <int Op, bool Vec, int NV>
 __global__ __launch_bounds__(kBlock) void rows_kernel(const float* __restrict__ x, float* __restrict__ out, int64_t rows,
                                                       int64_t len) {
     const int lane = threadIdx.x % kWave;
     const int64_t waves_per_grid = int64_t(gridDim.x) * (blockDim.x / kWave);
     for (int64_t r = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave; r < rows; r += waves_per_grid) {
         const float* row = x + r * len;
+        f4 v[NV > 0 ? NV : 1];
+        if (NV > 0) {
+#pragma unroll
+            for (int u = 0; u < NV; ++u) {
+                const int64_t a = int64_t(lane) * 4 + int64_t(u) * kWave * 4;
+                v[u] = a < len ? ld4(row + a) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
         if (Op == 0) {
             double acc = 0.0;
-            if (Vec) {
+            if (NV > 0) {
+#pragma unroll
+                for (int u = 0; u < NV; ++u) {
+                    if (int64_t(lane) * 4 + int64_t(u) * kWave * 4 < len) {
+                        acc += double(v[u].x);
+                        acc += double(v[u].y);
+                        acc += double(v[u].z);
+                        acc += double(v[u].w);
+                    }
+                }
+            } else if (Vec) {
                 for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
-                    const f4 v = ld4(row + a);
-                    acc += double(v.x);
-                    acc += double(v.y);
-                    acc += double(v.z);
-                    acc += double(v.w);
+                    const f4 w = ld4(row + a);
+                    acc += double(w.x);
+                    acc += double(w.y);
+                    acc += double(w.z);
+                    acc += double(w.w);
                 }
             } else {
                 for (int64_t a = lane; a < len; a += kWave) acc += double(row[a]);
@@ -81,22 +91,34 @@ __global__ __launch_bounds__(kBlock) void rows_kernel(const float* __restrict__ 
             acc = red::wave_sum(acc);
             if (lane == 0) out[r] = float(acc);
         } else {
-            Best b{0.0f, kNone};
-            if (Vec) {
+            Best b = red::no_best();
+            if (NV > 0) {
+#pragma unroll
+                for (int u = 0; u < NV; ++u) {
+                    const int a = lane * 4 + u * kWave * 4;
+                    if (a < len) {
+                        red::consider_ordered(b, v[u].x, a);
+                        red::consider_ordered(b, v[u].y, a + 1);
+                        red::consider_ordered(b, v[u].z, a + 2);
+                        red::consider_ordered(b, v[u].w, a + 3);
+                    }
+                }
+            } else if (Vec) {
                 for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
-                    const f4 v = ld4(row + a);
-                    consider(b, v.x, int(a));
-                    consider(b, v.y, int(a + 1));
-                    consider(b, v.z, int(a + 2));
-                    consider(b, v.w, int(a + 3));
+                    const f4 w = ld4(row + a);
+                    red::consider_ordered(b, w.x, int(a));
+                    red::consider_ordered(b, w.y, int(a + 1));
+                    red::consider_ordered(b, w.z, int(a + 2));
+                    red::consider_ordered(b, w.w, int(a + 3));
                 }
             } else {
-                for (int64_t a = lane; a < len; a += kWave) consider(b, row[a], int(a));
+                for (int64_t a = lane; a < len; a += kWave) red::consider_ordered(b, row[a], int(a));
             }
-            b = wave_best(b);
+            b = red::wave_best(b);
             if (lane == 0) {
-                const float first = row[0];
+                const float first = NV > 0 ? v[0].x : row[0];
                 if (first != first) b = Best{first, 0};
+                if (b.i == kNone) b.i = 0;
                 out[r] = Op == 1 ? b.v : float(b.i);
             }
         }
@@ -157,25 +179,25 @@ __global__ __launch_bounds__(kBlock) void colsum_tile_kernel(const float* __rest
     if (col < inner) {
         const float* base = x + o * len * inner + col;
         int64_t a = a0 + rl;
-        for (; a + 3 * kRowLanes < a1; a += 4 * kRowLanes) {  // four rows in flight
-            if (Vec) {
-                const f4 v0 = ld4(base + a * inner), v1 = ld4(base + (a + kRowLanes) * inner),
-                         v2 = ld4(base + (a + 2 * kRowLanes) * inner), v3 = ld4(base + (a + 3 * kRowLanes) * inner);
-                acc[0] += double(v0.x); acc[1] += double(v0.y); acc[2] += double(v0.z); acc[3] += double(v0.w);
-                acc[0] += double(v1.x); acc[1] += double(v1.y); acc[2] += double(v1.z); acc[3] += double(v1.w);
-                acc[0] += double(v2.x); acc[1] += double(v2.y); acc[2] += double(v2.z); acc[3] += double(v2.w);
-                acc[0] += double(v3.x); acc[1] += double(v3.y); acc[2] += double(v3.z); acc[3] += double(v3.w);
+        for (; a + 7 * kRowLanes < a1; a += 8 * kRowLanes) {  // eight rows in flight
+            if constexpr (Vec) {
+                f4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = ld4(base + (a + u * kRowLanes) * inner);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    acc[0] += double(v[u].x); acc[1] += double(v[u].y); acc[2] += double(v[u].z); acc[3] += double(v[u].w);
+                }
             } else {
-                const float v0 = base[a * inner], v1 = base[(a + kRowLanes) * inner],
-                            v2 = base[(a + 2 * kRowLanes) * inner], v3 = base[(a + 3 * kRowLanes) * inner];
-                acc[0] += double(v0);
-                acc[0] += double(v1);
-                acc[0] += double(v2);
-                acc[0] += double(v3);
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = base[(a + u * kRowLanes) * inner];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc[0] += double(v[u]);
             }
         }
         for (; a < a1; a += kRowLanes) {
-            if (Vec) {
+            if constexpr (Vec) {
                 const f4 v = ld4(base + a * inner);
                 acc[0] += double(v.x); acc[1] += double(v.y); acc[2] += double(v.z); acc[3] += double(v.w);
             } else {
@@ -376,13 +398,22 @@ int vc_hip_reduce_axis(const float* in, float* out, size_t outer_, size_t length
             // One wavefront per row; rows of < 64 elements leave lanes idle but stay correct.
             const bool vec = len % 4 == 0 && aligned16(in);
             const unsigned grid = unsigned(std::min<int64_t>((outer + 3) / 4, int64_t(d.cu_count) * 64));
-#define VC_ROWS(OP)                                                                                              \
-    if (vec) hipLaunchKernelGGL((rows_kernel<OP, true>), dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len); \
-    else hipLaunchKernelGGL((rows_kernel<OP, false>), dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len)
+            const int64_t nv = vec ? (len + kWave * 4 - 1) / (kWave * 4) : 0;
+#define VC_ROWS_NV(OP, VEC, NV) \
+    hipLaunchKernelGGL((rows_kernel<OP, VEC, NV>), dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len)
+#define VC_ROWS(OP)                                 \
+    if (!vec) VC_ROWS_NV(OP, false, 0);             \
+    else if (nv <= 1) VC_ROWS_NV(OP, true, 1);      \
+    else if (nv <= 2) VC_ROWS_NV(OP, true, 2);      \
+    else if (nv <= 4) VC_ROWS_NV(OP, true, 4);      \
+    else if (nv <= 8) VC_ROWS_NV(OP, true, 8);      \
+    else if (nv <= 16) VC_ROWS_NV(OP, true, 16);    \
+    else VC_ROWS_NV(OP, true, 0)
             if (op == VC_REDUCE_SUM) { VC_ROWS(0); }
             else if (op == VC_REDUCE_MAX) { VC_ROWS(1); }
             else { VC_ROWS(2); }
 #undef VC_ROWS
+#undef VC_ROWS_NV
             after_launch(label);
             p.done();
             return;

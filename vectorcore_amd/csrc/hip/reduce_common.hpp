@@ -1,6 +1,7 @@
 // Device helpers shared by the reduction and cross-entropy kernels:
-// wavefront/workgroup double sums with a fixed combine order, and the
-// two-stage full sum (fixed chunks, then one workgroup).
+// wavefront/workgroup double sums with a fixed combine order, the first
+// strict maximum of a row, and the two-stage full sum (fixed chunks, then one
+// workgroup).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -17,9 +18,106 @@ constexpr unsigned kBlock = 256;
 
 __device__ inline f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 
+// ---- cross-lane exchange ----------------------------------------------------
+// Butterfly partners of the six steps of a wavefront all-reduce: lane ^ 1 and
+// lane ^ 2 (DPP quad permutes), lane ^ 7 within 8 and lane ^ 15 within 16 (DPP
+// half-row and row mirrors), lane ^ 16 (ds_swizzle) and lane ^ 32
+// (ds_bpermute). After the six steps every lane holds the result.
+__device__ inline int lane_id() { return int(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u))); }
+
+template <int Step>
+__device__ inline uint32_t partner(uint32_t v, int lane) {
+    if constexpr (Step == 0) return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0xB1, 0xF, 0xF, false));
+    else if constexpr (Step == 1) return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x4E, 0xF, 0xF, false));
+    else if constexpr (Step == 2) return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x141, 0xF, 0xF, false));
+    else if constexpr (Step == 3) return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x140, 0xF, 0xF, false));
+    else if constexpr (Step == 4) return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), 0x401F));
+    else return uint32_t(__builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, int(v)));
+}
+
+template <int Step>
+__device__ inline double partner(double v, int lane) {
+    const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = partner<Step>(uint32_t(bits), lane), hi = partner<Step>(uint32_t(bits >> 32), lane);
+    return __builtin_bit_cast(double, lo | (hi << 32));
+}
+
+template <int Step>
+__device__ inline float partner(float v, int lane) {
+    return __builtin_bit_cast(float, partner<Step>(__builtin_bit_cast(uint32_t, v), lane));
+}
+
+template <int Step>
+__device__ inline int partner(int v, int lane) {
+    return int(partner<Step>(uint32_t(v), lane));
+}
+
+// Sum over the wavefront in a fixed order; every lane gets the same bits
+// (each step adds two partners' values, and fp addition commutes).
 __device__ inline double wave_sum(double v) {
-    for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    const int lane = lane_id();
+    v += partner<0>(v, lane);
+    v += partner<1>(v, lane);
+    v += partner<2>(v, lane);
+    v += partner<3>(v, lane);
+    v += partner<4>(v, lane);
+    v += partner<5>(v, lane);
     return v;
+}
+
+__device__ inline int wave_or(int v) {
+    const int lane = lane_id();
+    v |= partner<0>(v, lane);
+    v |= partner<1>(v, lane);
+    v |= partner<2>(v, lane);
+    v |= partner<3>(v, lane);
+    v |= partner<4>(v, lane);
+    v |= partner<5>(v, lane);
+    return v;
+}
+
+// ---- first strict maximum over a row ---------------------------------------
+// The reference scans a row with strict `>` from element 0
+// (src/cpu/cpu_backend.cpp:443-457): the first maximum wins and NaN never
+// replaces the running best. A lane visiting its elements in ascending index
+// order reproduces that with one compare, starting from {-inf, kNone}: NaN and
+// -inf never win. Lanes then combine by (larger value, then smaller index).
+// A row whose candidates were all -inf or NaN keeps kNone, which callers
+// resolve to element 0, where the reference's scan stays; a NaN element 0 is
+// the caller's check.
+constexpr int kNone = 0x7FFFFFFF;
+
+struct Best {
+    float v;
+    int i;
+};
+
+__device__ inline Best no_best() { return Best{-__builtin_huge_valf(), kNone}; }
+
+__device__ inline void consider_ordered(Best& b, float v, int i) {
+    if (v > b.v) {
+        b.v = v;
+        b.i = i;
+    }
+}
+
+template <int Step>
+__device__ inline Best combine_partner(Best b, int lane) {
+    const float ov = partner<Step>(b.v, lane);
+    const int oi = partner<Step>(b.i, lane);
+    const bool take = ov > b.v || (ov == b.v && oi < b.i);
+    return Best{take ? ov : b.v, take ? oi : b.i};
+}
+
+__device__ inline Best wave_best(Best b) {
+    const int lane = lane_id();
+    b = combine_partner<0>(b, lane);
+    b = combine_partner<1>(b, lane);
+    b = combine_partner<2>(b, lane);
+    b = combine_partner<3>(b, lane);
+    b = combine_partner<4>(b, lane);
+    b = combine_partner<5>(b, lane);
+    return b;
 }
 
 // Sum over the workgroup; the result is valid in thread 0.
@@ -42,31 +140,57 @@ inline int64_t sum_chunk(int64_t n) {
     return (chunk + 1023) / 1024 * 1024;
 }
 
-// Stage one: part[b] = sum of x[b*chunk, (b+1)*chunk) in double.
+struct Identity {
+    __device__ float operator()(float s) const { return s; }
+};
+
+// Sum of x[b0, b1) by one workgroup in double: thread t takes float4 t,
+// t + blockDim, ... (then the scalar tail); eight loads in flight.
 template <bool Vec>
-__global__ __launch_bounds__(kBlock) void sum_partial_kernel(const float* __restrict__ x, double* __restrict__ part,
-                                                             int64_t n, int64_t chunk) {
-    __shared__ double lds[kBlock / kWave];
-    const int64_t b0 = int64_t(blockIdx.x) * chunk, b1 = b0 + chunk < n ? b0 + chunk : n;
+__device__ inline double chunk_sum(const float* __restrict__ x, int64_t b0, int64_t b1) {
     double acc = 0.0;
     if (Vec) {  // b0 is a multiple of 4
         const int64_t v1 = b0 + (b1 - b0) / 4 * 4;
-        for (int64_t a = b0 + int64_t(threadIdx.x) * 4; a < v1; a += int64_t(blockDim.x) * 4) {
+        const int64_t stride = int64_t(blockDim.x) * 4;
+        int64_t a = b0 + int64_t(threadIdx.x) * 4;
+        for (; a + 7 * stride < v1; a += 8 * stride) {
+            f4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = ld4(x + a + u * stride);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                acc += double(v[u].x);
+                acc += double(v[u].y);
+                acc += double(v[u].z);
+                acc += double(v[u].w);
+            }
+        }
+        for (; a < v1; a += stride) {
             const f4 v = ld4(x + a);
             acc += double(v.x);
             acc += double(v.y);
             acc += double(v.z);
             acc += double(v.w);
         }
-        for (int64_t a = v1 + threadIdx.x; a < b1; a += blockDim.x) acc += double(x[a]);
+        for (int64_t t = v1 + threadIdx.x; t < b1; t += blockDim.x) acc += double(x[t]);
     } else {
-        for (int64_t a = b0 + threadIdx.x; a < b1; a += blockDim.x) acc += double(x[a]);
+        for (int64_t t = b0 + threadIdx.x; t < b1; t += blockDim.x) acc += double(x[t]);
     }
-    const double total = block_sum(acc, lds);
+    return acc;
+}
+
+// Stage one: part[b] = sum of x[b*chunk, (b+1)*chunk) in double.
+template <bool Vec>
+__global__ __launch_bounds__(kBlock) void sum_partial_kernel(const float* __restrict__ x, double* __restrict__ part,
+                                                             int64_t n, int64_t chunk) {
+    __shared__ double lds[kBlock / kWave];
+    const int64_t b0 = int64_t(blockIdx.x) * chunk, b1 = b0 + chunk < n ? b0 + chunk : n;
+    const double total = block_sum(chunk_sum<Vec>(x, b0, b1), lds);
     if (threadIdx.x == 0) part[blockIdx.x] = total;
 }
 
-// Stage two: out = finish(float(sum of the partials)).
+// Stage two: out = finish(float(sum of the partials)); thread t takes
+// b = t, t + blockDim, ..., then the fixed workgroup tree.
 template <class Finish>
 __global__ __launch_bounds__(kBlock) void sum_final_kernel(const double* __restrict__ part, float* __restrict__ out,
                                                            int64_t blocks, Finish finish) {
@@ -76,10 +200,6 @@ __global__ __launch_bounds__(kBlock) void sum_final_kernel(const double* __restr
     const double total = block_sum(acc, lds);
     if (threadIdx.x == 0) out[0] = finish(float(total));
 }
-
-struct Identity {
-    __device__ float operator()(float s) const { return s; }
-};
 
 }  // namespace red
 }  // namespace vchip

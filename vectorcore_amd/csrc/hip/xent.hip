@@ -28,46 +28,35 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 constexpr unsigned kBlock = 256;
 constexpr int kRowsPerBlock = kBlock / kWave;
-constexpr int kNone = std::numeric_limits<int>::max();
 
 __device__ inline f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 
-struct Best {
-    float v;
-    int i;
-};
-__device__ inline void consider(Best& b, float v, int i) {
-    if (v != v) return;
-    if (b.i == kNone || v > b.v || (v == b.v && i < b.i)) {
-        b.v = v;
-        b.i = i;
-    }
-}
-__device__ inline Best combine(Best a, Best b) {
-    if (b.i == kNone) return a;
-    if (a.i == kNone) return b;
-    return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
-}
+using red::Best;
+using red::kNone;
 
 __device__ inline float row_max(const float* row, int64_t len, int lane, bool vec) {
-    Best b{0.0f, kNone};
+    Best b = red::no_best();
     if (vec) {
         for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
             const f4 v = ld4(row + a);
-            consider(b, v.x, int(a));
-            consider(b, v.y, int(a + 1));
-            consider(b, v.z, int(a + 2));
-            consider(b, v.w, int(a + 3));
+            red::consider_ordered(b, v.x, int(a));
+            red::consider_ordered(b, v.y, int(a + 1));
+            red::consider_ordered(b, v.z, int(a + 2));
+            red::consider_ordered(b, v.w, int(a + 3));
         }
     } else {
-        for (int64_t a = lane; a < len; a += kWave) consider(b, row[a], int(a));
+        for (int64_t a = lane; a < len; a += kWave) red::consider_ordered(b, row[a], int(a));
     }
-    for (int off = kWave / 2; off > 0; off >>= 1) b = combine(b, Best{__shfl_xor(b.v, off, kWave), __shfl_xor(b.i, off, kWave)});
+    b = red::wave_best(b);
     const float first = row[0];
     return first != first ? first : b.v;  // max() keeps a NaN first element (src/cpu/cpu_backend.cpp:443-452)
 }
 
-template <bool Vec>
+// One wavefront per row. With NV > 0 the row (at most 256 NV classes, a
+// multiple of 4) is loaded once into registers, NV float4 per lane, all loads
+// in flight together; otherwise lanes stream it twice. Both visit each lane's
+// elements in the same order, so the results are the same bits.
+template <bool Vec, int NV>
 __global__ __launch_bounds__(kBlock) void xent_rows_kernel(const float* __restrict__ x, const int* __restrict__ targets,
                                                            int64_t rows, int64_t len, float* __restrict__ stats,
                                                            float* __restrict__ terms) {
@@ -75,32 +64,78 @@ __global__ __launch_bounds__(kBlock) void xent_rows_kernel(const float* __restri
     const int64_t r = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
     if (r >= rows) return;
     const float* row = x + r * len;
-    const float m = row_max(row, len, lane, Vec);
     const int t = targets[r];
+    float m;
     double acc = 0.0;
     int bad = 0;  // a non-target log-prob that is not finite
-    if (Vec) {
-        for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
-            const f4 v = ld4(row + a);
-            const float s0 = v.x - m, s1 = v.y - m, s2 = v.z - m, s3 = v.w - m;
-            acc += double(expf(s0));
-            acc += double(expf(s1));
-            acc += double(expf(s2));
-            acc += double(expf(s3));
-            bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) | (a + 2 != t && !isfinite(s2)) |
-                   (a + 3 != t && !isfinite(s3));
+    if (NV > 0) {
+        f4 v[NV > 0 ? NV : 1];
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const int64_t a = int64_t(lane) * 4 + int64_t(u) * kWave * 4;
+            v[u] = a < len ? ld4(row + a) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        Best b = red::no_best();
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const int a = lane * 4 + u * kWave * 4;
+            if (a < len) {
+                red::consider_ordered(b, v[u].x, a);
+                red::consider_ordered(b, v[u].y, a + 1);
+                red::consider_ordered(b, v[u].z, a + 2);
+                red::consider_ordered(b, v[u].w, a + 3);
+            }
+        }
+        b = red::wave_best(b);
+        const float first = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v[0].x)));
+        m = first != first ? first : b.v;  // max() keeps a NaN first element (src/cpu/cpu_backend.cpp:443-452)
+        bool nonfinite = false;  // any shifted value not finite, target included
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const int a = lane * 4 + u * kWave * 4;
+            if (a < len) {
+                const float s0 = v[u].x - m, s1 = v[u].y - m, s2 = v[u].z - m, s3 = v[u].w - m;
+                acc += double(expf(s0));
+                acc += double(expf(s1));
+                acc += double(expf(s2));
+                acc += double(expf(s3));
+                nonfinite |= !isfinite(s0) | !isfinite(s1) | !isfinite(s2) | !isfinite(s3);
+            }
+        }
+        if (__ballot(nonfinite) != 0) {  // rare: decide exactly, leaving the target out
+#pragma unroll
+            for (int u = 0; u < NV; ++u) {
+                const int a = lane * 4 + u * kWave * 4;
+                if (a < len) {
+                    const float s0 = v[u].x - m, s1 = v[u].y - m, s2 = v[u].z - m, s3 = v[u].w - m;
+                    bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) |
+                           (a + 2 != t && !isfinite(s2)) | (a + 3 != t && !isfinite(s3));
+                }
+            }
         }
     } else {
-        for (int64_t a = lane; a < len; a += kWave) {
-            const float s = row[a] - m;
-            acc += double(expf(s));
-            bad |= (a != t && !isfinite(s));
+        m = row_max(row, len, lane, Vec);
+        if (Vec) {
+            for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
+                const f4 v = ld4(row + a);
+                const float s0 = v.x - m, s1 = v.y - m, s2 = v.z - m, s3 = v.w - m;
+                acc += double(expf(s0));
+                acc += double(expf(s1));
+                acc += double(expf(s2));
+                acc += double(expf(s3));
+                bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) | (a + 2 != t && !isfinite(s2)) |
+                       (a + 3 != t && !isfinite(s3));
+            }
+        } else {
+            for (int64_t a = lane; a < len; a += kWave) {
+                const float s = row[a] - m;
+                acc += double(expf(s));
+                bad |= (a != t && !isfinite(s));
+            }
         }
     }
-    for (int off = kWave / 2; off > 0; off >>= 1) {
-        acc += __shfl_xor(acc, off, kWave);
-        bad |= __shfl_xor(bad, off, kWave);
-    }
+    acc = red::wave_sum(acc);
+    bad = red::wave_or(bad);
     if (lane == 0) {
         const float s = float(acc);
         const float L = logf(s);
@@ -176,12 +211,19 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         const bool vec = C % 4 == 0 && aligned16(logits);
         const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
         Profiled p("xent_forward", 0.0, 4.0 * double(R * C) + 4.0 * double(R) + 8.0 * double(R));
-        if (vec)
-            hipLaunchKernelGGL(xent_rows_kernel<true>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, R, C, row_stats,
-                               terms.as<float>());
-        else
-            hipLaunchKernelGGL(xent_rows_kernel<false>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, R, C,
-                               row_stats, terms.as<float>());
+        // Rows of up to 4096 classes are held in registers (NV float4 per lane).
+        const int64_t nv = vec ? (C + kWave * 4 - 1) / (kWave * 4) : 0;
+#define VC_XENT_ROWS(VEC, NV)                                                                                     \
+    hipLaunchKernelGGL((xent_rows_kernel<VEC, NV>), dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, R, C, \
+                       row_stats, terms.as<float>())
+        if (!vec) VC_XENT_ROWS(false, 0);
+        else if (nv <= 1) VC_XENT_ROWS(true, 1);
+        else if (nv <= 2) VC_XENT_ROWS(true, 2);
+        else if (nv <= 4) VC_XENT_ROWS(true, 4);
+        else if (nv <= 8) VC_XENT_ROWS(true, 8);
+        else if (nv <= 16) VC_XENT_ROWS(true, 16);
+        else VC_XENT_ROWS(true, 0);
+#undef VC_XENT_ROWS
         after_launch("xent_forward");
         // Row terms -> loss with the shared deterministic two-stage sum.
         const int64_t chunk = red::sum_chunk(R);

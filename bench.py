@@ -10,9 +10,11 @@ HBM. Each step ends with loss.item(), as the reference's train benchmark does
 buffers are recycled through the device pool.
 
 Prints one JSON line: whole-job train-steps/s, the backward-GEMM roofline
-(MFMA-bound; per-launch HIP events on the library stream over the timed
-region), the reduction bandwidth, and the reference CPU path timed on this
-host on a bounded slice of the same workload.
+(MFMA-bound; HIP events carried by the backward-GEMM dispatches on the library
+stream over the timed region, the only kernels timed there), the reduction
+bandwidth and forward-GEMM rate from a short breakdown pass that times every
+kernel, and the reference CPU path timed on this host on a bounded slice of
+the same workload.
 """
 
 from __future__ import annotations
@@ -32,6 +34,8 @@ BATCH = 8192
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 CPU_SAMPLE_ROWS = 1024         # CPU baseline: 1/8 of the batch, same network
+BWD_GEMM_LABELS = ("gemm_nt", "gemm_tn")  # dH = dY W^T and dW = H^T dY
+BREAKDOWN_STEPS = 5
 
 
 def log(*args):
@@ -76,8 +80,10 @@ def gpu_bench(steps: int, warmup: int, copy_calibration: bool = False):
         del src, _
     losses = [step() for _ in range(warmup)]
     allocs_before = vc.hip_pool_stats()["device_allocations"]
+    # Timed region. Only the backward GEMMs carry HIP events (as dispatch
+    # timestamps on the library stream), for the roofline.
     vc.synchronize()
-    vc.hip_profile(True)
+    vc.hip_profile(True, labels=list(BWD_GEMM_LABELS))
     vc.hip_profile_reset()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -85,12 +91,20 @@ def gpu_bench(steps: int, warmup: int, copy_calibration: bool = False):
     vc.synchronize()
     elapsed = time.perf_counter() - t0
     prof = vc.hip_profile_read()
-    vc.hip_profile(False)
     allocs_after = vc.hip_pool_stats()["device_allocations"]
+    # Breakdown pass after the timed region: every kernel carries events.
+    vc.hip_profile(True)
+    vc.hip_profile_reset()
+    breakdown_steps = max(1, min(steps, BREAKDOWN_STEPS))
+    for _ in range(breakdown_steps):
+        losses.append(step())
+    breakdown = vc.hip_profile_read()
+    vc.hip_profile(False)
     if not np.isfinite(losses[-1]) or not losses[-1] < losses[0]:
         raise SystemExit(f"bench.py: training did not make progress: {losses[0]} -> {losses[-1]}")
-    return dict(elapsed=elapsed, prof=prof, losses=losses, new_allocations=allocs_after - allocs_before,
-                device=vc.hip_device_name(), gemm_kernel=vc.hip_gemm_kernel())
+    return dict(elapsed=elapsed, prof=prof, breakdown=breakdown, breakdown_steps=breakdown_steps, losses=losses,
+                new_allocations=allocs_after - allocs_before, device=vc.hip_device_name(),
+                gemm_kernel=vc.hip_gemm_kernel())
 
 
 def cpu_baseline():
@@ -158,21 +172,24 @@ def main():
     r = gpu_bench(args.steps, args.warmup, args.copy_calibration)
     prof = r["prof"]
     ms_per_step = r["elapsed"] * 1e3 / args.steps
-    bwd = [v for k, v in prof.items() if k in ("gemm_nt", "gemm_tn")]
+    bwd = [v for k, v in prof.items() if k in BWD_GEMM_LABELS]
     bwd_flops = sum(v["flops"] for v in bwd)
     bwd_ms = sum(v["ms"] for v in bwd)
     bwd_launches = sum(v["launches"] for v in bwd)
     bwd_tflops = bwd_flops / bwd_ms / 1e9 if bwd_ms else None
-    red = prof.get("reduce_axis_sum", {})
+    # Per-kernel figures from the breakdown pass.
+    bd, nb = r["breakdown"], r["breakdown_steps"]
+    red = bd.get("reduce_axis_sum", {})
     reduce_gbs = red["bytes"] / red["ms"] / 1e6 if red.get("ms") else None
-    fwd = prof.get("gemm_nn", {})
+    fwd = bd.get("gemm_nn", {})
     fwd_tflops = fwd["flops"] / fwd["ms"] / 1e9 if fwd.get("ms") else None
-    device_ms = sum(v["ms"] for v in prof.values()) / args.steps
-    for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
+    device_ms = sum(v["ms"] for v in bd.values()) / nb
+    log(f"  breakdown pass ({nb} steps, every kernel timed):")
+    for k, v in sorted(bd.items(), key=lambda kv: -kv[1]["ms"]):
         rate = (f"{v['flops'] / v['ms'] / 1e9:7.1f} TFLOP/s" if v["flops"] and "gemm" in k
                 else f"{v['bytes'] / v['ms'] / 1e6:7.0f} GB/s")
-        log(f"  {k:22s} {v['launches'] / args.steps:5.1f}/step {v['ms'] / args.steps:8.3f} ms/step  {rate}")
-    log(f"  device time {device_ms:.3f} ms/step of {ms_per_step:.3f} ms/step wall")
+        log(f"  {k:22s} {v['launches'] / nb:5.1f}/step {v['ms'] / nb:8.3f} ms/step  {rate}")
+    log(f"  device time {device_ms:.3f} ms/step; timed region {ms_per_step:.3f} ms/step wall")
 
     traffic = load_traffic()
     roofline = {
@@ -206,6 +223,9 @@ def main():
         "reduce_gbs": round(reduce_gbs, 1) if reduce_gbs else None,
         "reduce_hbm_frac": round(reduce_gbs / HBM_PEAK_GBS, 4) if reduce_gbs else None,
         "device_ms_per_step": round(device_ms, 3),
+        "timing": "value and roofline: the timed steps, with events on the backward GEMMs only; "
+                  "fwd_gemm_tflops, reduce_gbs, device_ms_per_step: a breakdown pass of "
+                  f"{r['breakdown_steps']} further steps with every kernel timed",
         "pool_new_allocations_in_timed_steps": r["new_allocations"],
         "loss_first_last": [round(r["losses"][0], 5), round(r["losses"][-1], 5)],
         "device": r["device"],

@@ -169,9 +169,14 @@ int vc_hip_xent_backward(const float* logits, const int32_t* targets, const floa
                          const float* grad_loss, size_t rows, size_t classes, float* grad_logits);
 
 /* ---- measurement ------------------------------------------------------------- */
-/* When enabled, each kernel launch is bracketed by HIP events on the library
- * stream and its algorithmic work (FLOPs, bytes) is recorded by label. */
+/* When enabled, the kernels of each labelled entry-point call carry HIP
+ * events as dispatch timestamps on the library stream (no marker packets
+ * between kernels), and the call's algorithmic work (FLOPs, bytes) is
+ * recorded by label. Measurement support; no counterpart in the reference. */
 int vc_hip_profile_enable(int enable);
+/* Restricts the profiler to the comma-separated labels (e.g.
+ * "gemm_nt,gemm_tn"); NULL or "" profiles every label. */
+int vc_hip_profile_labels(const char* labels);
 int vc_hip_profile_reset(void);
 /* Waits for the stream, then reports the number of distinct labels. */
 int vc_hip_profile_count(size_t* labels);

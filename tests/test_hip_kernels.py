@@ -319,3 +319,31 @@ def test_errors_are_reported_not_thrown():
     with pytest.raises(ValueError):
         C.check(C.lib().vc_hip_reduce_axis(None, None, 1, 0, 1, C.MAX))
     assert b"empty axis" in C.lib().vc_hip_last_error()
+
+
+def test_profiler_times_selected_labels():
+    """The event profiler records labelled calls (dispatch timestamps) and can
+    be restricted to chosen labels; bench.py relies on both."""
+    x = C.Buffer.of(np.ones(1 << 20, np.float32))
+    y, s = C.Buffer((1 << 20,)), C.Buffer((1,))
+    try:
+        C.profile_labels(["reduce_sum"])
+        C.profile(True)
+        C.profile_reset()
+        C.check(C.lib().vc_hip_reduce_sum(x.ptr, 1 << 20, s.ptr))
+        C.check(C.lib().vc_hip_unary(x.ptr, y.ptr, 1 << 20, C.NEG))
+        got = C.profile_read()
+        assert set(got) == {"reduce_sum"}
+        assert got["reduce_sum"]["launches"] == 1 and got["reduce_sum"]["ms"] > 0
+        assert got["reduce_sum"]["bytes"] == 4.0 * (1 << 20)
+        C.profile_labels(None)
+        C.profile_reset()
+        C.check(C.lib().vc_hip_reduce_sum(x.ptr, 1 << 20, s.ptr))
+        C.check(C.lib().vc_hip_unary(x.ptr, y.ptr, 1 << 20, C.NEG))
+        got = C.profile_read()
+        assert {"reduce_sum", "unary_neg"} <= set(got)
+        assert all(v["ms"] > 0 for v in got.values())
+    finally:
+        C.profile(False)
+        C.profile_labels(None)
+    assert float(s.numpy()[0]) == float(1 << 20)

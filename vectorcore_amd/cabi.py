@@ -58,6 +58,7 @@ _SIGNATURES = {
     "vc_hip_xent_forward": ([_vp, _vp, _sz, _sz, _vp, _vp], _i),
     "vc_hip_xent_backward": ([_vp, _vp, _vp, _vp, _sz, _sz, _vp], _i),
     "vc_hip_profile_enable": ([_i], _i),
+    "vc_hip_profile_labels": ([ctypes.c_char_p], _i),
     "vc_hip_profile_reset": ([], _i),
     "vc_hip_profile_count": ([_szp], _i),
     "vc_hip_profile_entry": ([_sz, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_uint64),
@@ -154,6 +155,11 @@ class Buffer:
 
 def profile(enable: bool) -> None:
     check(lib().vc_hip_profile_enable(1 if enable else 0))
+
+
+def profile_labels(labels=None) -> None:
+    """Restrict the profiler to these labels (None: all)."""
+    check(lib().vc_hip_profile_labels(",".join(labels).encode() if labels else None))
 
 
 def profile_reset() -> None:

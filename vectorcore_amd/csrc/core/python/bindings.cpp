@@ -203,7 +203,16 @@ PYBIND11_MODULE(_vectorcore, m) {
         d["pooled_bytes"] = s.pooled_bytes;
         return d;
     });
-    m.def("hip_profile", [](bool enable) { check(vc_hip_profile_enable(enable ? 1 : 0)); });
+    m.def(
+        "hip_profile",
+        [](bool enable, std::optional<std::vector<std::string>> labels) {
+            std::string joined;
+            if (labels)
+                for (const auto& l : *labels) joined += (joined.empty() ? "" : ",") + l;
+            check(vc_hip_profile_labels(labels ? joined.c_str() : nullptr));
+            check(vc_hip_profile_enable(enable ? 1 : 0));
+        },
+        py::arg("enable"), py::arg("labels") = py::none());
     m.def("hip_profile_reset", [] { check(vc_hip_profile_reset()); });
     m.def("hip_profile_read", [] {
         std::size_t n = 0;

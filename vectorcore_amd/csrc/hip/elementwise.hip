@@ -219,9 +219,9 @@ void launch_map1(const char* label, const float* x, float* y, size_t n, F f, dou
     Profiled p(label, 0.0, bytes_per_elem * double(n));
     if (aligned16(x) && aligned16(y)) {
         const size_t n4 = n / 4, tail = n % 4;
-        hipLaunchKernelGGL(map1_kernel<F>, dim3(stream_grid(n4 ? n4 : 1)), dim3(kBlock), 0, d.stream, x, y, n4, tail, f);
+        launch(map1_kernel<F>, dim3(stream_grid(n4 ? n4 : 1)), dim3(kBlock), 0, d.stream, x, y, n4, tail, f);
     } else {
-        hipLaunchKernelGGL(map1_scalar_kernel<F>, dim3(stream_grid(n)), dim3(kBlock), 0, d.stream, x, y, n, f);
+        launch(map1_scalar_kernel<F>, dim3(stream_grid(n)), dim3(kBlock), 0, d.stream, x, y, n, f);
     }
     after_launch(label);
     p.done();
@@ -235,9 +235,9 @@ void launch_map2(const char* label, const float* a, const float* b, float* y, si
     Profiled p(label, 0.0, bytes_per_elem * double(n));
     if (aligned16(a) && aligned16(b) && aligned16(y)) {
         const size_t n4 = n / 4, tail = n % 4;
-        hipLaunchKernelGGL(map2_kernel<F>, dim3(stream_grid(n4 ? n4 : 1)), dim3(kBlock), 0, d.stream, a, b, y, n4, tail, f);
+        launch(map2_kernel<F>, dim3(stream_grid(n4 ? n4 : 1)), dim3(kBlock), 0, d.stream, a, b, y, n4, tail, f);
     } else {
-        hipLaunchKernelGGL(map2_scalar_kernel<F>, dim3(stream_grid(n)), dim3(kBlock), 0, d.stream, a, b, y, n, f);
+        launch(map2_scalar_kernel<F>, dim3(stream_grid(n)), dim3(kBlock), 0, d.stream, a, b, y, n, f);
     }
     after_launch(label);
     p.done();
@@ -260,10 +260,10 @@ void launch_binary(const float* a, const float* b, float* y, size_t n, const Bca
             Profiled p(label, 0.0, 8.0 * double(n));
             const size_t n4 = n / 4, tail = n % 4;
             if (scalar_first)
-                hipLaunchKernelGGL((scalar_operand_kernel<Op, true>), dim3(stream_grid(n4 ? n4 : 1)), dim3(kBlock), 0,
+                launch((scalar_operand_kernel<Op, true>), dim3(stream_grid(n4 ? n4 : 1)), dim3(kBlock), 0,
                                    d.stream, x, s, y, n4, tail);
             else
-                hipLaunchKernelGGL((scalar_operand_kernel<Op, false>), dim3(stream_grid(n4 ? n4 : 1)), dim3(kBlock), 0,
+                launch((scalar_operand_kernel<Op, false>), dim3(stream_grid(n4 ? n4 : 1)), dim3(kBlock), 0,
                                    d.stream, x, s, y, n4, tail);
             after_launch(label);
             p.done();
@@ -277,17 +277,17 @@ void launch_binary(const float* a, const float* b, float* y, size_t n, const Bca
         const unsigned grid = static_cast<unsigned>(std::min<int64_t>(rows, int64_t(d.cu_count) * 16));
         Profiled p(label, 0.0, 8.0 * double(n));
         if (vec)
-            hipLaunchKernelGGL((bcast2_kernel<Op, true>), dim3(grid), dim3(kBlock), 0, d.stream, a, b, y, rows, cols,
+            launch((bcast2_kernel<Op, true>), dim3(grid), dim3(kBlock), 0, d.stream, a, b, y, rows, cols,
                                m.a_stride[0], m.a_stride[1], m.b_stride[0], m.b_stride[1]);
         else
-            hipLaunchKernelGGL((bcast2_kernel<Op, false>), dim3(grid), dim3(kBlock), 0, d.stream, a, b, y, rows, cols,
+            launch((bcast2_kernel<Op, false>), dim3(grid), dim3(kBlock), 0, d.stream, a, b, y, rows, cols,
                                m.a_stride[0], m.a_stride[1], m.b_stride[0], m.b_stride[1]);
         after_launch(label);
         p.done();
         return;
     }
     Profiled p(label, 0.0, 8.0 * double(n));
-    hipLaunchKernelGGL(bcast_general_kernel<Op>, dim3(stream_grid(n)), dim3(kBlock), 0, d.stream, a, b, y, n, m);
+    launch(bcast_general_kernel<Op>, dim3(stream_grid(n)), dim3(kBlock), 0, d.stream, a, b, y, n, m);
     after_launch(label);
     p.done();
 }
@@ -310,7 +310,7 @@ int vc_hip_fill(float* out, size_t count, float value) {
         Device& d = require_device();
         if (count == 0) return;
         Profiled p("fill", 0.0, 4.0 * double(count));
-        hipLaunchKernelGGL(fill_kernel, dim3(stream_grid(count)), dim3(kBlock), 0, d.stream, out, count, value);
+        launch(fill_kernel, dim3(stream_grid(count)), dim3(kBlock), 0, d.stream, out, count, value);
         after_launch("fill");
         p.done();
     });
@@ -398,7 +398,7 @@ int vc_hip_div_backward(const float* grad, const float* a, const size_t* a_shape
         const Bcast m = make_bcast(a_shape, a_strides, a_rank, b_shape, b_strides, b_rank, out_shape, out_rank);
         if (n == 0 || (!grad_a && !grad_b)) return;
         Profiled p("div_backward", 0.0, 4.0 * double(n) * (2 + (grad_a ? 1 : 0) + (grad_b ? 1 : 0)));
-        hipLaunchKernelGGL(div_backward_kernel, dim3(stream_grid(n)), dim3(kBlock), 0, d.stream, grad, a, b, grad_a,
+        launch(div_backward_kernel, dim3(stream_grid(n)), dim3(kBlock), 0, d.stream, grad, a, b, grad_a,
                            grad_b, n, m);
         after_launch("div_backward");
         p.done();

@@ -376,11 +376,11 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
 template <bool TA, bool TB>
 void launch_variant(const GemmArgs& args, bool vec, bool simple, dim3 grid, hipStream_t stream) {
     if (simple) {
-        hipLaunchKernelGGL((gemm_simple_kernel<TA, TB>), grid, dim3(256), 0, stream, args);
+        launch((gemm_simple_kernel<TA, TB>), grid, dim3(256), 0, stream, args);
     } else if (vec) {
-        hipLaunchKernelGGL((gemm_mfma_kernel<TA, TB, true>), grid, dim3(kThreads), 0, stream, args);
+        launch((gemm_mfma_kernel<TA, TB, true>), grid, dim3(kThreads), 0, stream, args);
     } else {
-        hipLaunchKernelGGL((gemm_mfma_kernel<TA, TB, false>), grid, dim3(kThreads), 0, stream, args);
+        launch((gemm_mfma_kernel<TA, TB, false>), grid, dim3(kThreads), 0, stream, args);
     }
 }
 
@@ -463,7 +463,7 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     if (splits > 1) {
         after_launch(label);
         const int64_t total = batch * M * N;
-        hipLaunchKernelGGL(split_sum_kernel, dim3(unsigned(std::min<int64_t>((total + 255) / 256, int64_t(d.cu_count) * 16))),
+        launch(split_sum_kernel, dim3(unsigned(std::min<int64_t>((total + 255) / 256, int64_t(d.cu_count) * 16))),
                            dim3(256), 0, d.stream, partials.as<float>(), c, batch, M * N, splits);
     }
     after_launch(label);

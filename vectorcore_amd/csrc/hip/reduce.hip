@@ -333,13 +333,13 @@ void column_sum(Device& d, const float* in, float* out, int64_t outer, int64_t l
     Scratch part(size_t(segs * total) * sizeof(double));
     const dim3 grid(static_cast<unsigned>(blocks_x), static_cast<unsigned>(segs));
     if (vec)
-        hipLaunchKernelGGL(colsum_tile_kernel<true>, grid, dim3(kBlock), 0, d.stream, in, part.as<double>(), outer, len,
+        launch(colsum_tile_kernel<true>, grid, dim3(kBlock), 0, d.stream, in, part.as<double>(), outer, len,
                            inner, seg_len, chunks);
     else
-        hipLaunchKernelGGL(colsum_tile_kernel<false>, grid, dim3(kBlock), 0, d.stream, in, part.as<double>(), outer, len,
+        launch(colsum_tile_kernel<false>, grid, dim3(kBlock), 0, d.stream, in, part.as<double>(), outer, len,
                            inner, seg_len, chunks);
     after_launch(label);
-    hipLaunchKernelGGL(colsum_combine_kernel, dim3(unsigned((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, d.stream,
+    launch(colsum_combine_kernel, dim3(unsigned((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, d.stream,
                        part.as<double>(), out, total, segs);
     after_launch(label);
 }
@@ -362,14 +362,14 @@ int vc_hip_reduce_sum(const float* in, size_t count, float* out) {
         Profiled p("reduce_sum", double(n), 4.0 * double(n));
         if (blocks > 0) {
             if (aligned16(in))
-                hipLaunchKernelGGL(red::sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, in,
+                launch(red::sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, in,
                                    part.as<double>(), n, chunk);
             else
-                hipLaunchKernelGGL(red::sum_partial_kernel<false>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, in,
+                launch(red::sum_partial_kernel<false>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, in,
                                    part.as<double>(), n, chunk);
             after_launch("reduce_sum");
         }
-        hipLaunchKernelGGL(red::sum_final_kernel<red::Identity>, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), out,
+        launch(red::sum_final_kernel<red::Identity>, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), out,
                            blocks, red::Identity());
         after_launch("reduce_sum");
         p.done();
@@ -387,7 +387,7 @@ int vc_hip_reduce_axis(const float* in, float* out, size_t outer_, size_t length
         if (total == 0) return;
         const char* label = op == VC_REDUCE_SUM ? "reduce_axis_sum" : op == VC_REDUCE_MAX ? "reduce_axis_max" : "reduce_axis_argmax";
         if (len == 0) {  // sum over an empty axis is zero
-            hipLaunchKernelGGL(zero_kernel, dim3(grid_1d(size_t(total), kBlock, 1024)), dim3(kBlock), 0, d.stream, out, total);
+            launch(zero_kernel, dim3(grid_1d(size_t(total), kBlock, 1024)), dim3(kBlock), 0, d.stream, out, total);
             after_launch(label);
             return;
         }
@@ -400,7 +400,7 @@ int vc_hip_reduce_axis(const float* in, float* out, size_t outer_, size_t length
             const unsigned grid = unsigned(std::min<int64_t>((outer + 3) / 4, int64_t(d.cu_count) * 64));
             const int64_t nv = vec ? (len + kWave * 4 - 1) / (kWave * 4) : 0;
 #define VC_ROWS_NV(OP, VEC, NV) \
-    hipLaunchKernelGGL((rows_kernel<OP, VEC, NV>), dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len)
+    launch((rows_kernel<OP, VEC, NV>), dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len)
 #define VC_ROWS(OP)                                 \
     if (!vec) VC_ROWS_NV(OP, false, 0);             \
     else if (nv <= 1) VC_ROWS_NV(OP, true, 1);      \
@@ -420,9 +420,9 @@ int vc_hip_reduce_axis(const float* in, float* out, size_t outer_, size_t length
         }
         if (total >= target_threads || len < 64) {
             const unsigned grid = grid_1d(size_t(total), kBlock, unsigned(d.cu_count) * 64);
-            if (op == VC_REDUCE_SUM) hipLaunchKernelGGL(cols_kernel<0>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
-            else if (op == VC_REDUCE_MAX) hipLaunchKernelGGL(cols_kernel<1>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
-            else hipLaunchKernelGGL(cols_kernel<2>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
+            if (op == VC_REDUCE_SUM) launch(cols_kernel<0>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
+            else if (op == VC_REDUCE_MAX) launch(cols_kernel<1>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
+            else launch(cols_kernel<2>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
             after_launch(label);
             p.done();
             return;
@@ -440,14 +440,14 @@ int vc_hip_reduce_axis(const float* in, float* out, size_t outer_, size_t length
         const dim3 grid1(unsigned((total + kBlock - 1) / kBlock), unsigned(segs));
         const unsigned grid2 = unsigned((total + kBlock - 1) / kBlock);
         Scratch pv(size_t(segs * total) * sizeof(float)), pi(size_t(segs * total) * sizeof(int));
-        hipLaunchKernelGGL(cols_best_partial_kernel, grid1, dim3(kBlock), 0, d.stream, in, pv.as<float>(), pi.as<int>(), outer,
+        launch(cols_best_partial_kernel, grid1, dim3(kBlock), 0, d.stream, in, pv.as<float>(), pi.as<int>(), outer,
                            len, inner, seg_len);
         after_launch(label);
         if (op == VC_REDUCE_MAX)
-            hipLaunchKernelGGL(cols_best_combine_kernel<1>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv.as<float>(),
+            launch(cols_best_combine_kernel<1>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv.as<float>(),
                                pi.as<int>(), out, outer, len, inner, segs);
         else
-            hipLaunchKernelGGL(cols_best_combine_kernel<2>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv.as<float>(),
+            launch(cols_best_combine_kernel<2>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv.as<float>(),
                                pi.as<int>(), out, outer, len, inner, segs);
         after_launch(label);
         p.done();
@@ -460,7 +460,7 @@ int vc_hip_scatter_axis(const float* values, const float* indices, float* out, s
         const int64_t total = int64_t(outer * length * inner);
         if (total == 0) return;
         Profiled p("scatter_axis", 0.0, 4.0 * double(total + 2 * outer * inner));
-        hipLaunchKernelGGL(scatter_kernel, dim3(grid_1d(size_t(total), kBlock, unsigned(d.cu_count) * 16)), dim3(kBlock), 0,
+        launch(scatter_kernel, dim3(grid_1d(size_t(total), kBlock, unsigned(d.cu_count) * 16)), dim3(kBlock), 0,
                            d.stream, values, indices, out, int64_t(outer), int64_t(length), int64_t(inner));
         after_launch("scatter_axis");
         p.done();
@@ -475,7 +475,7 @@ int vc_hip_transpose_last2(const float* in, float* out, size_t batch, size_t row
         const dim3 grid(unsigned((cols + kTile - 1) / kTile), unsigned((rows + kTile - 1) / kTile),
                         unsigned(std::min<size_t>(batch, 65535)));
         Profiled p("transpose_last2", 0.0, 8.0 * double(batch * rows * cols));
-        hipLaunchKernelGGL(transpose_kernel, grid, dim3(kTile, 8), 0, d.stream, in, out, int64_t(batch), int64_t(rows),
+        launch(transpose_kernel, grid, dim3(kTile, 8), 0, d.stream, in, out, int64_t(batch), int64_t(rows),
                            int64_t(cols));
         after_launch("transpose_last2");
         p.done();

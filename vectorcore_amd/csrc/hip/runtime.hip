@@ -249,6 +249,7 @@ struct ProfAggregate {
 struct Profiler {
     std::mutex mu;
     bool enabled = false;
+    std::vector<std::string> only;  // empty: every label
     std::vector<std::string> labels;
     std::unordered_map<std::string, int> ids;
     std::vector<ProfRecord> done;
@@ -315,10 +316,19 @@ void after_launch(const char* label) {
     }
 }
 
+namespace {
+thread_local Profiled* t_profiled = nullptr;
+}
+
+Profiled* Profiled::current() { return t_profiled; }
+
 Profiled::Profiled(const char* label, double flops, double bytes) {
+    outer_ = t_profiled;
+    t_profiled = this;
     Profiler& p = profiler();
     std::lock_guard<std::mutex> lock(p.mu);
     if (!p.enabled) return;
+    if (!p.only.empty() && std::find(p.only.begin(), p.only.end(), label) == p.only.end()) return;
     auto it = p.ids.find(label);
     if (it == p.ids.end()) {
         label_ = static_cast<int>(p.labels.size());
@@ -331,15 +341,32 @@ Profiled::Profiled(const char* label, double flops, double bytes) {
     stop_ = p.event();
     flops_ = flops;
     bytes_ = bytes;
-    check_hip(hipEventRecord(start_, device().stream), "hipEventRecord");
+}
+
+Profiled::~Profiled() {
+    if (!popped_) t_profiled = outer_;
+    if (label_ >= 0) {  // abandoned (an error before done()): return the events unused
+        Profiler& p = profiler();
+        std::lock_guard<std::mutex> lock(p.mu);
+        p.spare.push_back(start_);
+        p.spare.push_back(stop_);
+    }
 }
 
 void Profiled::done() {
+    if (!popped_) {
+        t_profiled = outer_;
+        popped_ = true;
+    }
     if (label_ < 0) return;
     Profiler& p = profiler();
     std::lock_guard<std::mutex> lock(p.mu);
-    check_hip(hipEventRecord(stop_, device().stream), "hipEventRecord");
-    p.done.push_back(ProfRecord{label_, start_, stop_, flops_, bytes_});
+    if (started_) {
+        p.done.push_back(ProfRecord{label_, start_, stop_, flops_, bytes_});
+    } else {
+        p.spare.push_back(start_);
+        p.spare.push_back(stop_);
+    }
     label_ = -1;
 }
 
@@ -499,6 +526,25 @@ int vc_hip_profile_enable(int enable) {
         Profiler& p = profiler();
         std::lock_guard<std::mutex> lock(p.mu);
         p.enabled = enable != 0;
+    });
+}
+
+int vc_hip_profile_labels(const char* labels) {
+    return guard([&] {
+        Profiler& p = profiler();
+        std::lock_guard<std::mutex> lock(p.mu);
+        p.only.clear();
+        if (!labels) return;
+        std::string item;
+        for (const char* c = labels;; ++c) {
+            if (*c == ',' || *c == '\0') {
+                if (!item.empty()) p.only.push_back(item);
+                item.clear();
+                if (*c == '\0') break;
+            } else if (*c != ' ') {
+                item.push_back(*c);
+            }
+        }
     });
 }
 

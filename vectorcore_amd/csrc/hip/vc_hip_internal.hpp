@@ -3,6 +3,7 @@
 // checks and the optional per-launch event profiler.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -89,15 +90,43 @@ private:
 // --- profiler --------------------------------------------------------------
 // Usage around one launch:  Profiled p("label", flops, bytes);  kernel<<<...>>>;
 // p.done();  Both are no-ops unless profiling is enabled.
+// One labelled unit of work (an entry point's kernels) under the optional
+// profiler. Its timing comes from the kernels' own dispatch-packet timestamps:
+// launch() hands the first kernel of the scope the start event and every
+// kernel the stop event (hipExtLaunchKernelGGL), so profiling adds no marker
+// packets, and no bubbles, between kernels. Scopes nest per thread.
 class Profiled {
 public:
     Profiled(const char* label, double flops, double bytes);
-    void done();
+    ~Profiled();
+    Profiled(const Profiled&) = delete;
+    Profiled& operator=(const Profiled&) = delete;
+    void done();  // records the scope if any kernel carried its events
+    hipEvent_t start_event() {
+        if (label_ < 0 || started_) return nullptr;
+        started_ = true;
+        return start_;
+    }
+    hipEvent_t stop_event() const { return label_ < 0 ? nullptr : stop_; }
+    static Profiled* current();
+
 private:
     int label_ = -1;
+    bool started_ = false;
+    bool popped_ = false;
     hipEvent_t start_ = nullptr, stop_ = nullptr;
     double flops_ = 0, bytes_ = 0;
+    Profiled* outer_ = nullptr;
 };
+
+// Every kernel of the library is launched through here, on `stream`.
+template <typename F, typename... Args>
+inline void launch(F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t stream, Args... args) {
+    Profiled* p = Profiled::current();
+    hipEvent_t start = p ? p->start_event() : nullptr;
+    hipEvent_t stop = p ? p->stop_event() : nullptr;
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, start, stop, 0u, args...);
+}
 
 // --- launch-shape checks -----------------------------------------------------
 inline unsigned grid_1d(size_t items, unsigned block, unsigned max_blocks) {

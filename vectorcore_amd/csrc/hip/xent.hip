@@ -214,7 +214,7 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         // Rows of up to 4096 classes are held in registers (NV float4 per lane).
         const int64_t nv = vec ? (C + kWave * 4 - 1) / (kWave * 4) : 0;
 #define VC_XENT_ROWS(VEC, NV)                                                                                     \
-    hipLaunchKernelGGL((xent_rows_kernel<VEC, NV>), dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, R, C, \
+    launch((xent_rows_kernel<VEC, NV>), dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, R, C, \
                        row_stats, terms.as<float>())
         if (!vec) VC_XENT_ROWS(false, 0);
         else if (nv <= 1) VC_XENT_ROWS(true, 1);
@@ -229,10 +229,10 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         const int64_t chunk = red::sum_chunk(R);
         const int64_t blocks = (R + chunk - 1) / chunk;
         Scratch part(size_t(blocks) * sizeof(double));
-        hipLaunchKernelGGL(red::sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream,
+        launch(red::sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream,
                            terms.as<float>(), part.as<double>(), R, chunk);
         after_launch("xent_forward");
-        hipLaunchKernelGGL(red::sum_final_kernel<NegateDivide>, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), loss,
+        launch(red::sum_final_kernel<NegateDivide>, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), loss,
                            blocks, NegateDivide{float(R)});
         after_launch("xent_forward");
         p.done();
@@ -250,10 +250,10 @@ int vc_hip_xent_backward(const float* logits, const int32_t* targets, const floa
         const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
         Profiled p("xent_backward", 0.0, 8.0 * double(R * C) + 12.0 * double(R));
         if (vec)
-            hipLaunchKernelGGL(xent_backward_kernel<true>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, row_stats,
+            launch(xent_backward_kernel<true>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, row_stats,
                                grad_loss, R, C, grad_logits);
         else
-            hipLaunchKernelGGL(xent_backward_kernel<false>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets,
+            launch(xent_backward_kernel<false>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets,
                                row_stats, grad_loss, R, C, grad_logits);
         after_launch("xent_backward");
         p.done();

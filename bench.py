@@ -143,6 +143,158 @@ def cpu_baseline():
                 sample=f"C oracle, {rows}-row slice, one step, scaled x{BATCH // rows}")
 
 
+def _median_ms(fn, reps):
+    import statistics
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(times)
+
+
+def _profiled(vc, fn, labels=None):
+    """Per-label kernel aggregates of one call of fn (events on the kernels' dispatches)."""
+    vc.synchronize()
+    vc.hip_profile(True, labels=labels)
+    vc.hip_profile_reset()
+    fn()
+    out = vc.hip_profile_read()
+    vc.hip_profile(False)
+    return out
+
+
+def config_measurements(cpu: bool):
+    """The reference's other configurations on the hip device: throughput, the
+    roofline fraction of their kernels, and the reference CPU path on the same
+    inputs (whole calls, including the harness's host copies), in this run."""
+    import numpy as np
+
+    import vectorcore_amd as vc
+    from vectorcore_amd import workloads as W
+    ref = None
+    if cpu:
+        from oracle import kernels as K
+        ref = K.Reference() if K.Reference.available() else None
+    out = {}
+
+    # C1: spiral classifier train step (launch-bound; no roofline).
+    sp = W.spiral()
+    ps = []
+    for w, b in zip(sp["weights"], sp["biases"]):
+        ps += [vc.Tensor(w, requires_grad=True, device="hip"), vc.Tensor(b, requires_grad=True, device="hip")]
+    xs = vc.Tensor(sp["x"], device="hip")
+
+    def spiral_step():
+        loss = vc.cross_entropy((xs @ ps[0] + ps[1]).relu() @ ps[2] + ps[3], sp["targets"])
+        loss.backward()
+        vc.sgd_step(ps, sp["lr"])
+        vc.zero_grad(ps)
+        return loss.item()
+
+    for _ in range(5):
+        spiral_step()
+    c1 = {"workload": "spiral 300x2->64->3 train step, lr 1.0", "bound": "launch/latency",
+          "hip_steps_per_s": round(1e3 / _median_ms(spiral_step, 50), 1)}
+    if ref:
+        net = ref.mlp(sp["weights"], sp["biases"], sp["x"], sp["targets"])
+        net.step(sp["lr"])
+        c1["cpu_reference_steps_per_s"] = round(1e3 / _median_ms(lambda: net.step(sp["lr"]), 50), 1)
+    out["C1"] = c1
+
+    # C2: batched matmul backward, dA = dC B^T (NT) and dB = A^T dC (TN).
+    bm = W.bmm()
+    flops = 2.0 * 8 * 1024 ** 3
+    for name, bkey in (("C2", "b"), ("C2_broadcast_B", "b_shared")):
+        a = vc.Tensor(bm["a"], requires_grad=True, device="hip")
+        b = vc.Tensor(bm[bkey], requires_grad=True, device="hip")
+        dc = vc.Tensor(bm["dc"], device="hip")
+
+        def fwd_bwd():
+            (a @ b).backward(dc)
+            vc.zero_grad([a, b])
+            vc.synchronize()
+
+        fwd_bwd()
+        prof = _profiled(vc, fwd_bwd, labels=list(BWD_GEMM_LABELS))
+        ms = sum(v["ms"] for v in prof.values())
+        tflops = 2 * flops / ms / 1e9
+        c2 = {"workload": f"A [8,1024,1024] @ B {list(bm[bkey].shape)}, backward dA and dB",
+              "bound": "mfma", "bwd_gemm_tflops": round(tflops, 1), "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 3),
+              "bwd_gemm_ms": round(ms, 3), "hip_ms_forward_backward": round(_median_ms(fwd_bwd, 10), 3)}
+        if ref:
+            c2["cpu_reference_ms_forward_backward"] = round(
+                _median_ms(lambda: ref.matmul_backward(bm["a"], bm[bkey], bm["dc"]), 1), 1)
+        out[name] = c2
+        del a, b, dc
+
+    # C3: y = sigmoid(relu(x + bias)) * exp(0.1 x); backward for dx, dbias.
+    ac = W.activation()
+    x = vc.Tensor(ac["x"], requires_grad=True, device="hip")
+    bias = vc.Tensor(ac["bias"], requires_grad=True, device="hip")
+    dy = vc.Tensor(ac["dy"], device="hip")
+    holder = {}
+
+    def forward():
+        holder["y"] = (x + bias).relu().sigmoid() * (x * 0.1).exp()
+        vc.synchronize()
+
+    def backward():
+        holder["y"].backward(dy)
+        vc.synchronize()
+
+    forward(); backward(); vc.zero_grad([x, bias])
+    forward()
+    prof = _profiled(vc, backward)
+    vc.zero_grad([x, bias])
+    kms = sum(v["ms"] for v in prof.values())
+    kbytes = sum(v["bytes"] for v in prof.values())
+    min_bytes = 3 * 4096 * 4096 * 4 + 2 * 4096 * 4
+
+    def fwd_bwd3():
+        forward(); backward(); vc.zero_grad([x, bias])
+
+    c3 = {"workload": "x [4096,4096] + bias [1,4096]: sigmoid(relu) * exp(0.1 x), backward dx and dbias",
+          "bound": "hbm", "bwd_kernel_gbs": round(kbytes / kms / 1e6, 1),
+          "frac": round(kbytes / kms / 1e6 / HBM_PEAK_GBS, 3), "bwd_kernels_ms": round(kms, 3),
+          "bwd_kernel_launches": int(sum(v["launches"] for v in prof.values())),
+          "min_bytes_rate_gbs": round(min_bytes / kms / 1e6, 1),
+          "hip_ms_forward_backward": round(_median_ms(fwd_bwd3, 10), 3)}
+    if ref:
+        c3["cpu_reference_ms_forward_backward"] = round(
+            _median_ms(lambda: ref.activation_backward(ac["x"], ac["bias"], ac["dy"]), 1), 1)
+    out["C3"] = c3
+    del x, bias, dy, holder
+
+    # C4: mean softmax cross-entropy forward + backward, argmax over classes.
+    xe = W.xent()
+    lg = vc.Tensor(xe["logits"], requires_grad=True, device="hip")
+    tg = xe["targets"]
+
+    def ce():
+        loss = vc.cross_entropy(lg, tg)
+        loss.backward()
+        lg.detach().argmax(1)
+        vc.zero_grad([lg])
+        vc.synchronize()
+
+    ce()
+    prof = _profiled(vc, ce)
+    c4 = {"workload": "logits [32768,1000] N(0,4): loss, dlogits, argmax(1)", "bound": "hbm",
+          "hip_ms": round(_median_ms(ce, 10), 3)}
+    for label in ("xent_forward", "xent_backward", "reduce_axis_argmax"):
+        v = prof.get(label)
+        if v and v["ms"]:
+            gbs = v["bytes"] / v["ms"] / 1e6
+            c4[label] = {"ms": round(v["ms"], 4), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)}
+    if ref:
+        c4["cpu_reference_ms"] = round(_median_ms(lambda: ref.cross_entropy(xe["logits"], tg), 1), 1)
+    out["C4"] = c4
+    if ref:
+        out["cpu_reference_threads"] = ref.threads()
+    return out
+
+
 def load_traffic():
     """HBM bytes per launch of the dominant kernels, measured with rocprofv3
     FETCH_SIZE/WRITE_SIZE runs and kept in profiles/ (None when absent)."""
@@ -161,6 +313,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other configurations' measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first stream 256 MiB through a negate kernel (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -235,6 +388,10 @@ def main():
         t0 = time.perf_counter()
         out["cpu_baseline"] = cpu_baseline()
         log(f"  cpu baseline took {time.perf_counter() - t0:.1f} s")
+    if not args.no_configs:
+        t0 = time.perf_counter()
+        out["configs"] = config_measurements(cpu=not args.no_cpu_baseline)
+        log(f"  other configurations took {time.perf_counter() - t0:.1f} s")
     print(json.dumps(out), flush=True)
 
 

@@ -63,8 +63,9 @@ struct GemmArgs {
     int64_t reduce;                // products summed into each output
     int64_t a_rstride, b_rstride;
     int tiles_m, tiles_n;
-    int splits;                    // K split into this many ranges (partials summed afterwards)
-    int kt_per_split;              // BK slices per split
+    int splits;                    // work split into this many ranges (partials summed afterwards):
+    int kt_per_split;              //   reduce == 1: BK slices of K per split
+    int64_t r_per_split;           //   reduce > 1: products r per split
 };
 
 // Tile id -> (tile_m, tile_n) with the XCD remap and grouped order.
@@ -217,8 +218,15 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
         // access would become a per-lane loop).
         const int64_t z = uniform64(job / p.splits);
         const int split = __builtin_amdgcn_readfirstlane(int(job - z * p.splits));
-        const int kt_begin = split * p.kt_per_split;
-        const int kt_end = min(kt_total, kt_begin + p.kt_per_split);
+        int kt_begin = 0, kt_end = kt_total;
+        int64_t r_begin = 0, r_end = p.reduce;
+        if (p.reduce > 1) {
+            r_begin = split * p.r_per_split;
+            r_end = min(p.reduce, r_begin + p.r_per_split);
+        } else {
+            kt_begin = split * p.kt_per_split;
+            kt_end = min(kt_total, kt_begin + p.kt_per_split);
+        }
         const int64_t aoff = uniform64(p.table ? p.table[2 * z] : z * p.a_bstride);
         const int64_t boff = uniform64(p.table ? p.table[2 * z + 1] : z * p.b_bstride);
         f16v acc[2][2];
@@ -229,7 +237,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-        for (int64_t r = 0; r < p.reduce && kt_begin < kt_end; ++r) {
+        for (int64_t r = r_begin; r < r_end && kt_begin < kt_end; ++r) {
             TileLoader<AKC, Vec> la;
             TileLoader<BKC, Vec> lb;
             la.init(p.a + aoff + r * p.a_rstride, p.lda, m0, p.M, p.K);
@@ -438,17 +446,28 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     } else {
         vec = vec && a_bstride % 4 == 0 && b_bstride % 4 == 0;
     }
-    // Split K when the output has fewer tiles than two workgroups per CU and
-    // K is long: each split accumulates its K range into a partial matrix and
-    // a second pass sums the partials in split order (deterministic).
+    // Split the work when the output has fewer tiles than two workgroups per
+    // CU: a batch reduction (reduce > 1) splits into ranges of r, a long K into
+    // ranges of at least 32 slices (at most 4). Each split accumulates into its
+    // own partial matrix and a second pass sums the partials in split order
+    // (deterministic).
     const int kt_total = int((K + BK - 1) / BK);
     int splits = 1;
-    if (!simple && reduce == 1 && tiles * batch < 2 * int64_t(d.cu_count) && kt_total >= 64) {
-        splits = int(std::min<int64_t>((2 * int64_t(d.cu_count) + tiles * batch - 1) / (tiles * batch), 4));
-        splits = std::min(splits, kt_total / 32);
+    int64_t r_per_split = reduce;
+    const int64_t want = (2 * int64_t(d.cu_count) + tiles * batch - 1) / (tiles * batch);
+    if (!simple && tiles * batch < 2 * int64_t(d.cu_count)) {
+        if (reduce > 1) {
+            r_per_split = (reduce + std::min(want, reduce) - 1) / std::min(want, reduce);
+            splits = int((reduce + r_per_split - 1) / r_per_split);
+        } else if (kt_total >= 64) {
+            splits = int(std::min<int64_t>(want, 4));
+            splits = std::min(splits, kt_total / 32);
+        }
     }
+    if (batch * splits > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, "matmul batch too large");
     args.splits = splits;
     args.kt_per_split = (kt_total + splits - 1) / splits;
+    args.r_per_split = r_per_split;
     Scratch partials(splits > 1 ? size_t(batch * splits) * size_t(M * N) * sizeof(float) : 4);
     if (splits > 1) args.c = partials.as<float>();
     const dim3 grid(unsigned(tiles), unsigned(std::min<int64_t>(batch * splits, 65535)));

@@ -52,11 +52,114 @@ __device__ inline float row_max(const float* row, int64_t len, int lane, bool ve
     return first != first ? first : b.v;  // max() keeps a NaN first element (src/cpu/cpu_backend.cpp:443-452)
 }
 
-// One wavefront per row. With NV > 0 the row (at most 256 NV classes, a
-// multiple of 4) is loaded once into registers, NV float4 per lane, all loads
-// in flight together; otherwise lanes stream it twice. Both visit each lane's
-// elements in the same order, so the results are the same bits.
-template <bool Vec, int NV>
+// Lane 0: the row's statistics (max, exp-sum) and its loss term
+// shifted_t - log(s), NaN when a non-target log-prob is not finite.
+__device__ inline void write_row(const float* __restrict__ row, int64_t r, int64_t len, int t, float m, double acc,
+                                 int bad, float* __restrict__ stats, float* __restrict__ terms) {
+    const float s = float(acc);
+    const float L = logf(s);
+    float term;
+    if (t < 0 || int64_t(t) >= len) {
+        term = __builtin_nanf("");  // never reached with checked targets; no out-of-row read
+    } else {
+        const float shifted = row[t] - m;
+        term = bad ? __builtin_nanf("") : shifted - L;
+    }
+    stats[2 * r] = m;
+    stats[2 * r + 1] = s;
+    terms[r] = term;
+}
+
+// Row statistics and loss term of one row from values in registers (NV
+// float4 per lane; element a = 4 lane + 256 u + component, a multiple-of-4
+// row of at most 256 NV classes). Each lane visits its elements in ascending
+// order, as the streaming path does, so both give the same bits.
+template <int NV>
+__device__ inline void finish_row(const f4 (&v)[NV], const float* __restrict__ row, int64_t r, int64_t len, int t,
+                                  int lane, float* __restrict__ stats, float* __restrict__ terms) {
+    Best b = red::no_best();
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int a = lane * 4 + u * kWave * 4;
+        if (a < len) {
+            red::consider_ordered(b, v[u].x, a);
+            red::consider_ordered(b, v[u].y, a + 1);
+            red::consider_ordered(b, v[u].z, a + 2);
+            red::consider_ordered(b, v[u].w, a + 3);
+        }
+    }
+    b = red::wave_best(b);
+    const float first = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v[0].x)));
+    const float m = first != first ? first : b.v;  // max() keeps a NaN first element (src/cpu/cpu_backend.cpp:443-452)
+    // exp via the hardware exp2 (V_EXP_F32, 1 ulp) of s * log2(e): the
+    // rounding of the product adds |s| 2^-24 relative error, at most ~2e-7 on
+    // the terms within e^-3 of the row maximum, which carry the sum (s <= 0).
+    double acc = 0.0;
+    bool nonfinite = false;  // any shifted value not finite, target included
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int a = lane * 4 + u * kWave * 4;
+        if (a < len) {
+            const float s0 = v[u].x - m, s1 = v[u].y - m, s2 = v[u].z - m, s3 = v[u].w - m;
+            acc += double(__expf(s0));
+            acc += double(__expf(s1));
+            acc += double(__expf(s2));
+            acc += double(__expf(s3));
+            nonfinite |= !isfinite(s0) | !isfinite(s1) | !isfinite(s2) | !isfinite(s3);
+        }
+    }
+    int bad = 0;  // a non-target log-prob that is not finite
+    if (__ballot(nonfinite) != 0) {  // rare: decide exactly, leaving the target out
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const int a = lane * 4 + u * kWave * 4;
+            if (a < len) {
+                const float s0 = v[u].x - m, s1 = v[u].y - m, s2 = v[u].z - m, s3 = v[u].w - m;
+                bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) | (a + 2 != t && !isfinite(s2)) |
+                       (a + 3 != t && !isfinite(s3));
+            }
+        }
+    }
+    acc = red::wave_sum(acc);
+    bad = red::wave_or(bad);
+    if (lane == 0) write_row(row, r, len, t, m, acc, bad, stats, terms);
+}
+
+template <int NV>
+__device__ inline void load_row(f4 (&v)[NV], const float* __restrict__ row, int64_t len, int lane) {
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int64_t a = int64_t(lane) * 4 + int64_t(u) * kWave * 4;
+        v[u] = a < len ? ld4(row + a) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
+// Rows held in registers. Each wavefront walks rows r, r + W, ... (W
+// wavefronts in the grid) and loads its next row before working on the
+// current one, so memory latency overlaps the exp work of the row before.
+template <int NV>
+__global__ __launch_bounds__(kBlock) void xent_rows_cached_kernel(const float* __restrict__ x,
+                                                                  const int* __restrict__ targets, int64_t rows,
+                                                                  int64_t len, float* __restrict__ stats,
+                                                                  float* __restrict__ terms) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t first = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
+    const int64_t waves = int64_t(gridDim.x) * kRowsPerBlock;
+    if (first >= rows) return;
+    f4 cur[NV], next[NV];
+    load_row(cur, x + first * len, len, lane);
+    for (int64_t r = first; r < rows; r += waves) {
+        const int64_t rn = r + waves;
+        if (rn < rows) load_row(next, x + rn * len, len, lane);
+        finish_row(cur, x + r * len, r, len, targets[r], lane, stats, terms);
+#pragma unroll
+        for (int u = 0; u < NV; ++u) cur[u] = next[u];
+    }
+}
+
+// One wavefront per row, streaming the row twice (rows too long for
+// registers, or not 16-byte aligned).
+template <bool Vec>
 __global__ __launch_bounds__(kBlock) void xent_rows_kernel(const float* __restrict__ x, const int* __restrict__ targets,
                                                            int64_t rows, int64_t len, float* __restrict__ stats,
                                                            float* __restrict__ terms) {
@@ -65,91 +168,30 @@ __global__ __launch_bounds__(kBlock) void xent_rows_kernel(const float* __restri
     if (r >= rows) return;
     const float* row = x + r * len;
     const int t = targets[r];
-    float m;
+    const float m = row_max(row, len, lane, Vec);
     double acc = 0.0;
     int bad = 0;  // a non-target log-prob that is not finite
-    if (NV > 0) {
-        f4 v[NV > 0 ? NV : 1];
-#pragma unroll
-        for (int u = 0; u < NV; ++u) {
-            const int64_t a = int64_t(lane) * 4 + int64_t(u) * kWave * 4;
-            v[u] = a < len ? ld4(row + a) : f4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-        Best b = red::no_best();
-#pragma unroll
-        for (int u = 0; u < NV; ++u) {
-            const int a = lane * 4 + u * kWave * 4;
-            if (a < len) {
-                red::consider_ordered(b, v[u].x, a);
-                red::consider_ordered(b, v[u].y, a + 1);
-                red::consider_ordered(b, v[u].z, a + 2);
-                red::consider_ordered(b, v[u].w, a + 3);
-            }
-        }
-        b = red::wave_best(b);
-        const float first = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v[0].x)));
-        m = first != first ? first : b.v;  // max() keeps a NaN first element (src/cpu/cpu_backend.cpp:443-452)
-        bool nonfinite = false;  // any shifted value not finite, target included
-#pragma unroll
-        for (int u = 0; u < NV; ++u) {
-            const int a = lane * 4 + u * kWave * 4;
-            if (a < len) {
-                const float s0 = v[u].x - m, s1 = v[u].y - m, s2 = v[u].z - m, s3 = v[u].w - m;
-                acc += double(expf(s0));
-                acc += double(expf(s1));
-                acc += double(expf(s2));
-                acc += double(expf(s3));
-                nonfinite |= !isfinite(s0) | !isfinite(s1) | !isfinite(s2) | !isfinite(s3);
-            }
-        }
-        if (__ballot(nonfinite) != 0) {  // rare: decide exactly, leaving the target out
-#pragma unroll
-            for (int u = 0; u < NV; ++u) {
-                const int a = lane * 4 + u * kWave * 4;
-                if (a < len) {
-                    const float s0 = v[u].x - m, s1 = v[u].y - m, s2 = v[u].z - m, s3 = v[u].w - m;
-                    bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) |
-                           (a + 2 != t && !isfinite(s2)) | (a + 3 != t && !isfinite(s3));
-                }
-            }
+    if (Vec) {
+        for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
+            const f4 v = ld4(row + a);
+            const float s0 = v.x - m, s1 = v.y - m, s2 = v.z - m, s3 = v.w - m;
+            acc += double(expf(s0));
+            acc += double(expf(s1));
+            acc += double(expf(s2));
+            acc += double(expf(s3));
+            bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) | (a + 2 != t && !isfinite(s2)) |
+                   (a + 3 != t && !isfinite(s3));
         }
     } else {
-        m = row_max(row, len, lane, Vec);
-        if (Vec) {
-            for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
-                const f4 v = ld4(row + a);
-                const float s0 = v.x - m, s1 = v.y - m, s2 = v.z - m, s3 = v.w - m;
-                acc += double(expf(s0));
-                acc += double(expf(s1));
-                acc += double(expf(s2));
-                acc += double(expf(s3));
-                bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) | (a + 2 != t && !isfinite(s2)) |
-                       (a + 3 != t && !isfinite(s3));
-            }
-        } else {
-            for (int64_t a = lane; a < len; a += kWave) {
-                const float s = row[a] - m;
-                acc += double(expf(s));
-                bad |= (a != t && !isfinite(s));
-            }
+        for (int64_t a = lane; a < len; a += kWave) {
+            const float s = row[a] - m;
+            acc += double(expf(s));
+            bad |= (a != t && !isfinite(s));
         }
     }
     acc = red::wave_sum(acc);
     bad = red::wave_or(bad);
-    if (lane == 0) {
-        const float s = float(acc);
-        const float L = logf(s);
-        float term;
-        if (t < 0 || int64_t(t) >= len) {
-            term = __builtin_nanf("");  // never reached with checked targets; no out-of-row read
-        } else {
-            const float shifted = row[t] - m;
-            term = bad ? __builtin_nanf("") : shifted - L;
-        }
-        stats[2 * r] = m;
-        stats[2 * r + 1] = s;
-        terms[r] = term;
-    }
+    if (lane == 0) write_row(row, r, len, t, m, acc, bad, stats, terms);
 }
 
 // loss = -(float)(sum of row terms) / (float)rows: negate, then divide, as
@@ -211,18 +253,22 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         const bool vec = C % 4 == 0 && aligned16(logits);
         const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
         Profiled p("xent_forward", 0.0, 4.0 * double(R * C) + 4.0 * double(R) + 8.0 * double(R));
-        // Rows of up to 4096 classes are held in registers (NV float4 per lane).
+        // Rows of up to 4096 classes are held in registers (NV float4 per lane),
+        // with at most 8 wavefronts per SIMD walking the rows.
         const int64_t nv = vec ? (C + kWave * 4 - 1) / (kWave * 4) : 0;
-#define VC_XENT_ROWS(VEC, NV)                                                                                     \
-    launch((xent_rows_kernel<VEC, NV>), dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, R, C, \
-                       row_stats, terms.as<float>())
-        if (!vec) VC_XENT_ROWS(false, 0);
-        else if (nv <= 1) VC_XENT_ROWS(true, 1);
-        else if (nv <= 2) VC_XENT_ROWS(true, 2);
-        else if (nv <= 4) VC_XENT_ROWS(true, 4);
-        else if (nv <= 8) VC_XENT_ROWS(true, 8);
-        else if (nv <= 16) VC_XENT_ROWS(true, 16);
-        else VC_XENT_ROWS(true, 0);
+        const unsigned cached_grid = unsigned(std::min<int64_t>((R + kRowsPerBlock - 1) / kRowsPerBlock,
+                                                                int64_t(d.cu_count) * 8));
+#define VC_XENT_ROWS(NV)                                                                                       \
+    launch((xent_rows_cached_kernel<NV>), dim3(cached_grid), dim3(kBlock), 0, d.stream, logits, targets, R, C, \
+           row_stats, terms.as<float>())
+        if (!vec || nv > 16)
+            launch((vec ? xent_rows_kernel<true> : xent_rows_kernel<false>), dim3(grid), dim3(kBlock), 0, d.stream,
+                   logits, targets, R, C, row_stats, terms.as<float>());
+        else if (nv <= 1) VC_XENT_ROWS(1);
+        else if (nv <= 2) VC_XENT_ROWS(2);
+        else if (nv <= 4) VC_XENT_ROWS(4);
+        else if (nv <= 8) VC_XENT_ROWS(8);
+        else VC_XENT_ROWS(16);
 #undef VC_XENT_ROWS
         after_launch("xent_forward");
         // Row terms -> loss with the shared deterministic two-stage sum.

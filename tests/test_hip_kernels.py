@@ -90,6 +90,26 @@ def test_gemm_split_k_long_reductions():
             np.testing.assert_array_equal(run_gemm(a, b, m, k, n, ta, tb, batch=batch), got)
 
 
+def test_gemm_relu_mask_is_gemm_then_relu_backward_bitexact():
+    """vc_hip_matmul_relu_mask = vc_hip_matmul, then vc_hip_relu_backward with
+    the same mask source: same bits, including a split-K shape and a batch."""
+    rng = np.random.default_rng(21)
+    for (m, k, n, batch) in ((257, 129, 383, 1), (130, 8192, 64, 1), (64, 96, 72, 3)):
+        for ta, tb in ((0, 0), (0, 1), (1, 0), (1, 1)):
+            a = rng.uniform(-1, 1, size=(batch,) + ((k, m) if ta else (m, k))).astype(np.float32)
+            b = rng.uniform(-1, 1, size=(batch,) + ((n, k) if tb else (k, n))).astype(np.float32)
+            x = rng.standard_normal((batch, m, n)).astype(np.float32)
+            x.flat[:5] = [0.0, -0.0, np.nan, np.inf, -np.inf]
+            da, db, dx = C.Buffer.of(a), C.Buffer.of(b), C.Buffer.of(x)
+            fused, plain, masked = C.Buffer((batch, m, n)), C.Buffer((batch, m, n)), C.Buffer((batch, m, n))
+            ao, bo = C.sizes([z * m * k for z in range(batch)]), C.sizes([z * k * n for z in range(batch)])
+            C.check(C.lib().vc_hip_matmul_relu_mask(da.ptr, db.ptr, fused.ptr, m, k, n, ao, bo, batch, ta, tb, dx.ptr))
+            C.check(C.lib().vc_hip_matmul(da.ptr, db.ptr, plain.ptr, m, k, n, ao, bo, batch, ta, tb))
+            C.check(C.lib().vc_hip_relu_backward(plain.ptr, dx.ptr, masked.ptr, batch * m * n))
+            np.testing.assert_array_equal(fused.numpy(), masked.numpy(), err_msg=f"{m}x{k}x{n} ta={ta} tb={tb}")
+            assert (fused.numpy() == 0).any() and (fused.numpy() != 0).any()
+
+
 def test_gemm_batch_reduce_matches_summed_products():
     """dB of a batch-broadcast B: sum_z A[z]^T dC[z] in one launch."""
     bm = W.bmm(batch=3, m=96, k=80, n=72, seed=1)

@@ -294,6 +294,58 @@ def test_mutation_after_backward_is_allowed_and_training_converges(device):
     assert abs(w.item() - 2.0) < 1e-3
 
 
+# --- ReLU rule folded into the product that feeds it -----------------------------------
+# On hip the engine lets a matrix product apply the mask of the ReLU whose
+# output it alone consumes (and which keeps no gradient), in the same kernel.
+
+
+def _relu_net(device, retain=False, reuse=False, seed=7):
+    rng = np.random.default_rng(seed)
+    x = T(rng.standard_normal((64, 48)), device)
+    w1 = T(rng.standard_normal((48, 96)) * 0.2, device, True)
+    b1 = T(rng.standard_normal(96) * 0.1, device, True)
+    w2 = T(rng.standard_normal((96, 40)) * 0.2, device, True)
+    h = (x @ w1 + b1).relu()
+    if retain:
+        h.retain_grad()
+    y = h @ w2
+    if reuse:  # h feeds two products
+        y = y + h @ (w2 * 0.5)
+    (y * y).sum().backward()
+    return h, [w1, b1, w2]
+
+
+def test_relu_fold_gives_the_unfolded_bits(device):
+    _, folded = _relu_net(device)
+    h, plain = _relu_net(device, retain=True)  # a kept gradient turns the fold off
+    for p, q in zip(folded, plain):
+        np.testing.assert_array_equal(npy(p.grad), npy(q.grad))
+    _, cpu = _relu_net("cpu")
+    for p, q in zip(folded, cpu):
+        np.testing.assert_allclose(npy(p.grad), npy(q.grad), rtol=1e-4, atol=1e-4)
+    # the kept gradient is the one before the mask: dense where h == 0 too
+    assert (npy(h.grad) != 0).sum() > (npy(h) > 0).sum()
+
+
+def test_relu_fold_with_a_shared_activation(device):
+    _, got = _relu_net(device, reuse=True)
+    _, cpu = _relu_net("cpu", reuse=True)
+    for p, q in zip(got, cpu):
+        np.testing.assert_allclose(npy(p.grad), npy(q.grad), rtol=1e-4, atol=1e-4)
+
+
+def test_relu_fold_keeps_the_version_check(device):
+    w = T(np.linspace(-1, 1, 12).reshape(3, 4), device, True)
+    w2 = T(np.ones((4, 2)), device, True)
+    loss = (w.relu() @ w2).sum()
+    ws = w.detach()
+    ws.requires_grad = True
+    (ws * 1.0).sum().backward()
+    vc.sgd_step([ws], 1.0)  # rewrites the ReLU's saved input
+    with pytest.raises(RuntimeError, match="modified in place"):
+        loss.backward()
+
+
 # --- finite-difference gradcheck (test_autograd_correctness.py:47-143) ----------------
 
 

@@ -50,6 +50,7 @@ _SIGNATURES = {
     "vc_hip_log_backward": ([_vp, _vp, _vp, _sz], _i),
     "vc_hip_div_backward": ([_vp, _vp, _szp, _szp, _sz, _vp, _szp, _szp, _sz, _szp, _sz, _vp, _vp], _i),
     "vc_hip_matmul": ([_vp, _vp, _vp, _sz, _sz, _sz, _szp, _szp, _sz, _i, _i], _i),
+    "vc_hip_matmul_relu_mask": ([_vp, _vp, _vp, _sz, _sz, _sz, _szp, _szp, _sz, _i, _i, _vp], _i),
     "vc_hip_matmul_reduce": ([_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _i], _i),
     "vc_hip_transpose_last2": ([_vp, _vp, _sz, _sz, _sz], _i),
     "vc_hip_reduce_sum": ([_vp, _sz, _vp], _i),

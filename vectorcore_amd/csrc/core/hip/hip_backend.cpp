@@ -224,6 +224,29 @@ std::shared_ptr<Storage> HipBackend::matmul(const Storage& a, std::size_t a_offs
     return out;
 }
 
+std::shared_ptr<Storage> HipBackend::matmul_relu_mask(const Storage& a, std::size_t a_offset, const Storage& b,
+                                                      std::size_t b_offset, std::size_t m, std::size_t k, std::size_t n,
+                                                      const std::vector<std::size_t>& a_offsets,
+                                                      const std::vector<std::size_t>& b_offsets, bool trans_a,
+                                                      bool trans_b, const Storage& relu_input,
+                                                      std::size_t relu_offset) {
+    require(*this);
+    if (a_offsets.size() != b_offsets.size() || a_offsets.empty())
+        throw std::invalid_argument("HIP matmul needs one A and B offset per batch");
+    const std::size_t batch = a_offsets.size();
+    auto out = fresh(batch * m * n);
+    if (batch * m * n == 0) return out;
+    if (k == 0) {  // empty inner dimension: the product, masked or not, is +0
+        check(vc_hip_fill(out->ptr(), batch * m * n, 0.0F), "HIP fill failed");
+        return out;
+    }
+    check(vc_hip_matmul_relu_mask(dptr(a, a_offset), dptr(b, b_offset), out->ptr(), m, k, n, a_offsets.data(),
+                                  b_offsets.data(), batch, trans_a ? 1 : 0, trans_b ? 1 : 0,
+                                  dptr(relu_input, relu_offset)),
+          "HIP matmul failed");
+    return out;
+}
+
 std::shared_ptr<Storage> HipBackend::matmul_reduce(const Storage& a, std::size_t a_offset, const Storage& b,
                                                    std::size_t b_offset, std::size_t m, std::size_t k, std::size_t n,
                                                    std::size_t count, std::size_t a_stride, std::size_t b_stride,

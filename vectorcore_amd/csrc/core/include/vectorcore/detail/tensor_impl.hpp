@@ -16,7 +16,24 @@ struct TensorImpl;
 struct GradFn {
     std::vector<std::shared_ptr<TensorImpl>> parents;
     std::function<std::vector<Tensor>(const Tensor&)> backward;
+    // Set by relu(): its saved input (unpacking checks the version). Lets the
+    // engine offer the ReLU mask to the node that produces this node's
+    // upstream gradient (see ReluMaskOffer).
+    std::function<Tensor()> relu_input;
 };
+
+// The engine's offer to the backward rule it is about to run: parent 0 of
+// that node is a ReLU output with no other consumer in the graph and no
+// retained gradient, so the rule may return parent 0's gradient already
+// multiplied by [relu input > 0] (the ReLU rule's own arithmetic) and set
+// `taken`; the engine then passes that gradient through the ReLU node as is.
+struct ReluMaskOffer {
+    std::function<Tensor()> relu_input;
+    bool taken = false;
+};
+// The offer in effect on this thread, or null.
+ReluMaskOffer* relu_mask_offer();
+void set_relu_mask_offer(ReluMaskOffer* offer);
 
 struct TensorImpl {
     std::shared_ptr<Storage> storage;

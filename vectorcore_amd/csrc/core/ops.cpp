@@ -14,6 +14,7 @@
 #include "vectorcore/storage.hpp"
 
 #include <cstdint>
+#include <optional>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -173,9 +174,18 @@ MatmulPlan plan_matmul(const Tensor& a, const Tensor& b, bool trans_a, bool tran
 }
 
 // op(A) @ op(B) without a gradient rule (transposes read in place).
-Tensor matmul_kernel(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b) {
+Tensor matmul_kernel(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b,
+                     const Tensor* relu_input = nullptr) {
     require_same_device(a, b);
     const MatmulPlan p = plan_matmul(a, b, trans_a, trans_b);
+    if (relu_input) {  // hip only: the product times [relu_input > 0], relu_input shaped like the product
+        auto s = hip().matmul_relu_mask(st(a), off(a), st(b), off(b), p.m, p.k, p.n, p.a_offsets, p.b_offsets,
+                                        trans_a, trans_b, st(*relu_input), off(*relu_input));
+        Shape out_shape = p.out_batch;
+        out_shape.push_back(p.m);
+        out_shape.push_back(p.n);
+        return detail::make_tensor(std::move(s), out_shape, false);
+    }
     std::shared_ptr<Storage> s;
     switch (a.device().type) {
         case DeviceType::CPU: {
@@ -294,7 +304,25 @@ Tensor matmul(const Tensor& a, const Tensor& b) {
                                              static_cast<std::size_t>(b_step), false, true);
                 grads[0] = detail::make_tensor(std::move(s), as);
             } else if (na) {
-                grads[0] = detail::sum_to_shape(matmul_kernel(g, bv, false, true), as);
+                // The engine may offer A's ReLU mask (A = relu(x) feeding only
+                // this product): dA * [x > 0] comes out of the same kernel.
+                detail::ReluMaskOffer* offer = detail::relu_mask_offer();
+                Shape product = p.out_batch;
+                product.push_back(p.m);
+                product.push_back(p.k);
+                std::optional<Tensor> relu_input;
+                if (offer && product == as) {
+                    relu_input = offer->relu_input();
+                    if (relu_input->device() != Device::hip() || relu_input->shape() != as ||
+                        relu_input->strides() != contiguous_strides(as))
+                        relu_input.reset();
+                }
+                if (relu_input) {
+                    grads[0] = matmul_kernel(g, bv, false, true, &*relu_input);
+                    offer->taken = true;
+                } else {
+                    grads[0] = detail::sum_to_shape(matmul_kernel(g, bv, false, true), as);
+                }
             }
             if (nb && p.batch > 1 && numel(p.b_batch) == 1 && a_step >= 0) {
                 // dB = sum_z A_z^T @ dY_z.
@@ -437,6 +465,7 @@ Tensor relu(const Tensor& v) {
     detail::attach_grad_fn(out, {v}, [saved](const Tensor& g) {
         return std::vector<Tensor>{activation_grad(HipBackend::Activation::Relu, g, saved.unpack())};
     });
+    if (out.impl()->grad_fn) out.impl()->grad_fn->relu_input = [saved] { return saved.unpack(); };
     return out;
 }
 

@@ -282,8 +282,15 @@ void Tensor::backward(const Tensor& gradient) const {
         stack.pop_back();
     }
 
+    // How many graph nodes feed a gradient to each node.
+    std::unordered_map<detail::TensorImpl*, int> consumers;
+    for (const auto& node : order)
+        if (node->grad_fn)
+            for (const auto& parent : node->grad_fn->parents) ++consumers[parent.get()];
+
     NoGradGuard guard;
     std::unordered_map<detail::TensorImpl*, Tensor> pending;
+    std::unordered_set<detail::TensorImpl*> premasked;  // ReLU outputs whose gradient arrived masked
     pending.emplace(impl_.get(), gradient.detach());
     for (auto it = order.rbegin(); it != order.rend(); ++it) {
         const auto& node = *it;
@@ -295,7 +302,31 @@ void Tensor::backward(const Tensor& gradient) const {
             node->grad = node->grad ? (detail::from_impl(node->grad) + upstream).detach().impl() : upstream.detach().impl();
         }
         if (!node->grad_fn) continue;
-        auto grads = node->grad_fn->backward(upstream);
+        std::vector<Tensor> grads;
+        if (premasked.count(node.get())) {
+            grads.push_back(upstream);  // the producer already applied this ReLU's rule
+        } else {
+            // Offer the ReLU mask of parent 0 when its gradient comes from this
+            // node alone and is not kept: the rule may fuse it into its kernel
+            // (hip products do). The gradient is the same either way.
+            const auto& first = node->grad_fn->parents.empty() ? nullptr : node->grad_fn->parents[0];
+            detail::ReluMaskOffer offer;
+            const bool offered = first && upstream.device() == Device::hip() && first->grad_fn &&
+                                 first->grad_fn->relu_input && first->requires_grad && !first->leaf &&
+                                 !first->retains_grad && consumers[first.get()] == 1;
+            if (offered) {
+                offer.relu_input = first->grad_fn->relu_input;
+                detail::set_relu_mask_offer(&offer);
+            }
+            try {
+                grads = node->grad_fn->backward(upstream);
+            } catch (...) {
+                detail::set_relu_mask_offer(nullptr);
+                throw;
+            }
+            detail::set_relu_mask_offer(nullptr);
+            if (offered && offer.taken) premasked.insert(first.get());
+        }
         if (grads.size() != node->grad_fn->parents.size())
             throw std::logic_error("autograd function returned the wrong number of gradients");
         for (std::size_t i = 0; i < grads.size(); ++i) {

@@ -66,6 +66,7 @@ struct GemmArgs {
     int splits;                    // work split into this many ranges (partials summed afterwards):
     int kt_per_split;              //   reduce == 1: BK slices of K per split
     int64_t r_per_split;           //   reduce > 1: products r per split
+    const float* relu_mask;        // null, or [batch][M][N]: C *= [relu_mask > 0] (fused ReLU backward)
 };
 
 // Tile id -> (tile_m, tile_n) with the XCD remap and grouped order.
@@ -190,8 +191,12 @@ __device__ inline void read_part(const float* __restrict__ lds, int off, int g, 
     }
 }
 
+// Vector-load variants fit two workgroups per CU (<= 256 VGPRs). The scalar-load
+// variants (misaligned operands only) keep 32 element loads and their masks
+// in flight, so they get the register file of one workgroup per CU rather
+// than spilling.
 template <bool TA, bool TB, bool Vec>
-__global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
+__global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmArgs p) {
     // Two LDS stages. Step kt multiplies out of stage cur while its first k-group
     // also stores slice kt + 1 (in registers since step kt - 1) into the other
     // stage and issues the global loads of slice kt + 2. Fragments are read one
@@ -315,10 +320,42 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
         // Epilogue: buffer stores relative to the tile origin; rows/columns
         // outside C are pointed out of range and dropped by the hardware. With a
         // split K each split writes its own partial matrix.
+        // The fused ReLU mask (g * [x > 0], the backward rule's arithmetic) is
+        // applied here unless K was split, in which case split_sum_kernel does.
         float* C = p.c + (p.splits > 1 ? job : z) * int64_t(p.M) * p.N;
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(C + int64_t(m0) * p.N + n0);
+        const bool masked = p.relu_mask && p.splits == 1;
+        const __amdgpu_buffer_rsrc_t rm =
+            make_rsrc((masked ? p.relu_mask + z * int64_t(p.M) * p.N : C) + int64_t(m0) * p.N + n0);
         const int row_lim = p.M - m0, col_lim = p.N - n0;
         const int row0 = wm + 4 * (lane >> 5);
+        if (masked) {  // all 64 mask loads in flight before the first use
+            f16v x[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int col = wn + 32 * j + (lane & 31);
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int row = row0 + 32 * i + 8 * (v >> 2) + (v & 3);
+                        const bool ok = row < row_lim && col < col_lim;
+                        x[i][j][v] = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(
+                                       rm, ok ? uint32_t(row * p.N + col) * 4u : kOutOfRange, 0, 0));
+                    }
+                }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const float xv = x[i][j][v];
+                        const float value = acc[i][j][v];
+                        acc[i][j][v] = value * (xv > 0.0f ? 1.0f : 0.0f);
+                    }
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -337,9 +374,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs p) {
     }
 }
 
-// Split-K combine: c[z][i] = sum over s of part[z][s][i], in split order.
+// Split combine: c[z][i] = sum over s of part[z][s][i], in split order, then
+// the fused ReLU mask when there is one.
 __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ part, float* __restrict__ c,
-                                                        int64_t batch, int64_t mn, int splits) {
+                                                        int64_t batch, int64_t mn, int splits,
+                                                        const float* __restrict__ relu_mask) {
     const int64_t total = batch * mn;
     const int64_t stride = int64_t(gridDim.x) * blockDim.x;
     for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
@@ -347,6 +386,7 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
         const float* src = part + z * splits * mn + i;
         float acc = src[0];
         for (int s = 1; s < splits; ++s) acc += src[int64_t(s) * mn];
+        if (relu_mask) acc = acc * (relu_mask[t] > 0.0f ? 1.0f : 0.0f);
         c[t] = acc;
     }
 }
@@ -377,7 +417,11 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
                 __syncthreads();
             }
         }
-        if (row < p.M && col < p.N) p.c[z * p.M * p.N + row * p.N + col] = acc;
+        if (row < p.M && col < p.N) {
+            const int64_t t = z * p.M * p.N + row * p.N + col;
+            if (p.relu_mask) acc = acc * (p.relu_mask[t] > 0.0f ? 1.0f : 0.0f);
+            p.c[t] = acc;
+        }
     }
 }
 
@@ -399,7 +443,7 @@ const char* variant_label(bool ta, bool tb) {
 // offsets: nullptr for the affine mode (a_bstride / b_bstride).
 void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t a_bstride,
           int64_t b_bstride, const std::vector<int64_t>* offsets, int64_t reduce, int64_t a_rstride, int64_t b_rstride,
-          bool ta, bool tb) {
+          bool ta, bool tb, const float* relu_mask = nullptr) {
     Device& d = require_device();
     if (M < 0 || N < 0 || K < 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "negative matrix dimension");
     if (M == 0 || N == 0 || batch == 0) return;
@@ -473,7 +517,9 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     const dim3 grid(unsigned(tiles), unsigned(std::min<int64_t>(batch * splits, 65535)));
     const char* label = variant_label(ta, tb);
     const double flops = 2.0 * double(M) * double(N) * double(K) * double(batch) * double(reduce);
-    const double bytes = 4.0 * (double(M * K + K * N) * double(reduce) + double(M * N)) * double(batch);
+    args.relu_mask = relu_mask;
+    const double bytes =
+        4.0 * (double(M * K + K * N) * double(reduce) + double(M * N) * (relu_mask ? 2.0 : 1.0)) * double(batch);
     Profiled prof(label, flops, bytes);
     if (ta && tb) launch_variant<true, true>(args, vec, simple, grid, d.stream);
     else if (ta) launch_variant<true, false>(args, vec, simple, grid, d.stream);
@@ -483,10 +529,35 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
         after_launch(label);
         const int64_t total = batch * M * N;
         launch(split_sum_kernel, dim3(unsigned(std::min<int64_t>((total + 255) / 256, int64_t(d.cu_count) * 16))),
-                           dim3(256), 0, d.stream, partials.as<float>(), c, batch, M * N, splits);
+                           dim3(256), 0, d.stream, partials.as<float>(), c, batch, M * N, splits, relu_mask);
     }
     after_launch(label);
     prof.done();
+}
+
+// Per-batch offsets as the reference passes them: affine ones (the common
+// batched and broadcast cases) go as strides, anything else as a table.
+void matmul_offsets(const float* a, const float* b, float* c, size_t m, size_t k, size_t n, const size_t* a_offsets,
+                    const size_t* b_offsets, size_t batch, int trans_a, int trans_b, const float* relu_mask) {
+    if (batch == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul needs one A and B offset per batch");
+    if (!a_offsets || !b_offsets) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul: null offsets");
+    const int64_t sa = batch > 1 ? int64_t(a_offsets[1]) - int64_t(a_offsets[0]) : 0;
+    const int64_t sb = batch > 1 ? int64_t(b_offsets[1]) - int64_t(b_offsets[0]) : 0;
+    bool affine = a_offsets[0] == 0 && b_offsets[0] == 0;
+    for (size_t z = 0; affine && z < batch; ++z)
+        affine = int64_t(a_offsets[z]) == int64_t(z) * sa && int64_t(b_offsets[z]) == int64_t(z) * sb;
+    if (affine) {
+        gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), int64_t(batch), sa, sb, nullptr, 1, 0, 0, trans_a != 0,
+             trans_b != 0, relu_mask);
+    } else {
+        std::vector<int64_t> table(2 * batch);
+        for (size_t z = 0; z < batch; ++z) {
+            table[2 * z] = int64_t(a_offsets[z]);
+            table[2 * z + 1] = int64_t(b_offsets[z]);
+        }
+        gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), int64_t(batch), 0, 0, &table, 1, 0, 0, trans_a != 0,
+             trans_b != 0, relu_mask);
+    }
 }
 
 }  // namespace
@@ -498,27 +569,15 @@ extern "C" {
 
 int vc_hip_matmul(const float* a, const float* b, float* c, size_t m, size_t k, size_t n, const size_t* a_offsets,
                   const size_t* b_offsets, size_t batch, int trans_a, int trans_b) {
+    return guard([&] { matmul_offsets(a, b, c, m, k, n, a_offsets, b_offsets, batch, trans_a, trans_b, nullptr); });
+}
+
+int vc_hip_matmul_relu_mask(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                            const size_t* a_offsets, const size_t* b_offsets, size_t batch, int trans_a, int trans_b,
+                            const float* relu_input) {
     return guard([&] {
-        if (batch == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul needs one A and B offset per batch");
-        if (!a_offsets || !b_offsets) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul: null offsets");
-        // Affine offsets (the common batched and broadcast cases) go as strides.
-        const int64_t sa = batch > 1 ? int64_t(a_offsets[1]) - int64_t(a_offsets[0]) : 0;
-        const int64_t sb = batch > 1 ? int64_t(b_offsets[1]) - int64_t(b_offsets[0]) : 0;
-        bool affine = a_offsets[0] == 0 && b_offsets[0] == 0;
-        for (size_t z = 0; affine && z < batch; ++z)
-            affine = int64_t(a_offsets[z]) == int64_t(z) * sa && int64_t(b_offsets[z]) == int64_t(z) * sb;
-        if (affine) {
-            gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), int64_t(batch), sa, sb, nullptr, 1, 0, 0, trans_a != 0,
-                 trans_b != 0);
-        } else {
-            std::vector<int64_t> table(2 * batch);
-            for (size_t z = 0; z < batch; ++z) {
-                table[2 * z] = int64_t(a_offsets[z]);
-                table[2 * z + 1] = int64_t(b_offsets[z]);
-            }
-            gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), int64_t(batch), 0, 0, &table, 1, 0, 0, trans_a != 0,
-                 trans_b != 0);
-        }
+        if (!relu_input) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask: null ReLU input");
+        matmul_offsets(a, b, c, m, k, n, a_offsets, b_offsets, batch, trans_a, trans_b, relu_input);
     });
 }
 

@@ -15,13 +15,12 @@
 // with few tiles and a long K split K into ranges whose partial products are
 // summed in range order by a second pass.
 //
-// LDS layout follows each operand's contiguous axis, so no transposing stores:
-//  - k-contiguous operand (A in NN/NT, B in NT): [128][32 + 4] floats; a lane
-//    reads 4 consecutive k with one ds_read_b128, feeding 4 MFMA steps. The
-//    +4 padding makes the 8-lane phases of those reads conflict-free.
-//  - m/n-contiguous operand (A in TN, B in NN/TN): [32][128 + 8] floats; a
-//    lane reads one value per MFMA step (ds_read_b32); +8 keeps the two
-//    half-waves (k and k+4) on different banks.
+// LDS holds both operand tiles k-contiguous, [128][32 + 4] floats, so a lane
+// reads 4 consecutive k with one ds_read_b128, feeding 4 MFMA steps (the +4
+// padding keeps those reads conflict-free). A k-contiguous operand (A in
+// NN/NT, B in NT/TT) is stored as loaded; an m/n-contiguous one (A in TN/TT,
+// B in NN/TN) is loaded as 4 x 4 blocks (4 k-rows of 4 m/n per thread) and
+// stored transposed.
 // Within each group of 8 k, half-wave 0 of a step takes k = 8g + s and
 // half-wave 1 takes k = 8g + 4 + s (s = 0..3): a fixed permutation of the
 // summation index applied identically to A and B.
@@ -43,11 +42,8 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, BK = 32;
 constexpr int kThreads = 256;
-constexpr int kPadK = 4;   // k-contiguous LDS row padding
-constexpr int kPadMN = 8;  // m/n-contiguous LDS row padding
-constexpr int kLdsK = BM * (BK + kPadK);   // floats, k-contiguous tile
-constexpr int kLdsMN = BK * (BM + kPadMN); // floats, m/n-contiguous tile
-constexpr int kLdsTile = kLdsK > kLdsMN ? kLdsK : kLdsMN;
+constexpr int kPadK = 4;                     // LDS row padding
+constexpr int kLdsTile = BM * (BK + kPadK);  // floats per operand tile: [128][32 + 4], k-contiguous
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 
@@ -102,11 +98,14 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
 
 // Global -> register loader for one operand tile (128 along m/n, BK along k),
 // in four 16-byte slots per thread. Slot q of a k-contiguous operand is row
-// mn0 + 32 q, k k0 (8 threads per 32-float row); slot q of an m/n-contiguous
-// operand is k-row k0 + 8 q, column mn0 (32 threads per 128-float row). Each
-// thread keeps one byte offset (slot 0); slots step by a uniform amount passed
-// as the instruction's scalar offset. The tile origin is uniform (scalar
-// registers). Edges are masked by pointing a slot out of range.
+// mn0 + 32 q, k k0..k0+3 (8 threads per 32-float row). Slot q of an
+// m/n-contiguous operand is k-row k0 + q, columns mn0..mn0+3: a thread's four
+// slots are a 4 x 4 block, and the 8 threads of one m/n range hold k 0..31, so
+// a load instruction reads 128-byte row segments and a transposed store
+// writes one whole LDS row per 8 lanes (no bank conflicts). Each thread keeps
+// one byte offset (slot 0); slots step by a uniform amount passed as the
+// instruction's scalar offset. The tile origin is uniform (scalar registers).
+// Edges are masked by pointing a slot out of range.
 // KC: operand contiguous along k.
 template <bool KC, bool Vec>
 struct TileLoader {
@@ -129,10 +128,10 @@ struct TileLoader {
             mn0 = t / (BK / 4);
             k0 = (t % (BK / 4)) * 4;
             qstep = 32u * ld4;
-        } else {
-            k0 = t / (BM / 4);
-            mn0 = (t % (BM / 4)) * 4;
-            qstep = 8u * ld4;
+        } else {  // eight threads cover one 128-byte row segment along m/n
+            k0 = (t % (BK / 4)) * 4;
+            mn0 = (t / (BK / 4)) * 4;
+            qstep = ld4;
         }
         voff = KC ? uint32_t(mn0) * ld4 + uint32_t(k0) * 4u : uint32_t(k0) * ld4 + uint32_t(mn0) * 4u;
     }
@@ -141,7 +140,7 @@ struct TileLoader {
 
     // Slot q of slice kt. Slices past K read as zeros without touching memory.
     __device__ f4 load(__amdgpu_buffer_rsrc_t rs, int kt, int q) const {
-        const int k = kt * BK + k0 + (KC ? 0 : 8 * q);
+        const int k = kt * BK + k0 + (KC ? 0 : q);
         const int mn = mn0 + (KC ? 32 * q : 0);
         const uint32_t soff = uint32_t(q) * qstep;
         if (Vec) {
@@ -158,37 +157,37 @@ struct TileLoader {
         return v;
     }
 
-    // Byte offset of this thread's slot 0 in an LDS stage; slot q adds
-    // q * lds_qstep.
-    __device__ uint32_t lds_off() const {
-        return KC ? uint32_t(mn0 * (BK + kPadK) + k0) * 4u : uint32_t(k0 * (BM + kPadMN) + mn0) * 4u;
-    }
-    static constexpr uint32_t lds_qstep = KC ? 32u * (BK + kPadK) * 4u : 8u * (BM + kPadMN) * 4u;
+    // Byte offset in an LDS stage of this thread's first 16-byte store (row
+    // mn0, k k0); store q adds q * lds_qstep.
+    __device__ uint32_t lds_off() const { return uint32_t(mn0 * (BK + kPadK) + k0) * 4u; }
+    static constexpr uint32_t lds_qstep = KC ? 32u * (BK + kPadK) * 4u : uint32_t(BK + kPadK) * 4u;
 };
 
-// Slot q of a slice into an LDS stage (`off` from TileLoader::lds_off).
+// Store q (0..3) of this thread's slice registers into an LDS stage (`off`
+// from TileLoader::lds_off). Both operands sit k-contiguous in LDS: a
+// k-contiguous slot goes as it is; an m/n-contiguous operand's 4 x 4 block
+// goes transposed, store q being row mn0 + q = component q of the four slots.
 template <bool KC, bool Vec>
-__device__ inline void store_slot(char* __restrict__ lds, uint32_t off, const f4& v, int q) {
-    *reinterpret_cast<f4*>(lds + off + q * TileLoader<KC, Vec>::lds_qstep) = v;
+__device__ inline void store_slot(char* __restrict__ lds, uint32_t off, const f4 (&v)[4], int q) {
+    f4 row;
+    if (KC) {
+        row = v[q];
+    } else {
+        row = f4{v[0][q], v[1][q], v[2][q], v[3][q]};
+    }
+    *reinterpret_cast<f4*>(lds + off + q * TileLoader<KC, Vec>::lds_qstep) = row;
 }
 
 // Part s (0..3) of the fragments of k-group g for the wave's two 32-row
 // blocks at `off` and `off + 32`: frag[b][s'] is the value for MFMA step s'.
-// A k-contiguous operand reads block s's 4 values with one ds_read_b128 (at
-// parts `first` and `first + 1`); an m/n-contiguous operand reads step s of
-// both blocks.
-template <bool KC>
+// Block b's 4 values come with one ds_read_b128, at parts `first` and
+// `first + 1` (A uses parts 0-1, B parts 2-3, so each part issues one read).
 __device__ inline void read_part(const float* __restrict__ lds, int off, int g, int lane, int s, int first,
                                  f4 (&frag)[2]) {
     const int r = off + (lane & 31);
     const int kb = g * 8 + 4 * (lane >> 5);
-    if (KC) {
-        const int b = s - first;
-        if (b == 0 || b == 1) frag[b] = *reinterpret_cast<const f4*>(lds + (r + 32 * b) * (BK + kPadK) + kb);
-    } else {
-        frag[0][s] = lds[(kb + s) * (BM + kPadMN) + r];
-        frag[1][s] = lds[(kb + s) * (BM + kPadMN) + r + 32];
-    }
+    const int b = s - first;
+    if (b == 0 || b == 1) frag[b] = *reinterpret_cast<const f4*>(lds + (r + 32 * b) * (BK + kPadK) + kb);
 }
 
 // Vector-load variants fit two workgroups per CU (<= 256 VGPRs). The scalar-load
@@ -255,8 +254,13 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
                 const __amdgpu_buffer_rsrc_t sa = la.slice(kt_begin), sb = lb.slice(kt_begin);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    store_slot<AKC, Vec>(lds_a, a_st, la.load(sa, kt_begin, q), q);
-                    store_slot<BKC, Vec>(lds_b, b_st, lb.load(sb, kt_begin, q), q);
+                    ra[q] = la.load(sa, kt_begin, q);
+                    rb[q] = lb.load(sb, kt_begin, q);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    store_slot<AKC, Vec>(lds_a, a_st, ra, q);
+                    store_slot<BKC, Vec>(lds_b, b_st, rb, q);
                 }
                 const __amdgpu_buffer_rsrc_t na = la.slice(kt_begin + 1), nb = lb.slice(kt_begin + 1);
 #pragma unroll
@@ -269,8 +273,8 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
             f4 fa[2][2], fb[2][2];  // [k-group parity][32-row block]
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                read_part<AKC>(As[0], wm, 0, lane, s, 0, fa[0]);
-                read_part<BKC>(Bs[0], wn, 0, lane, s, 2, fb[0]);
+                read_part(As[0], wm, 0, lane, s, 0, fa[0]);
+                read_part(Bs[0], wn, 0, lane, s, 2, fb[0]);
             }
             for (int kt = kt_begin; kt < kt_end; ++kt) {
                 const int cur = (kt - kt_begin) & 1;
@@ -289,18 +293,22 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
                     if (g == BK / 8 - 1) __syncthreads();
 #pragma unroll
                     for (int s = 0; s < 4; ++s) {
+                        // Store q of the next stage at step q of k-group 0. A
+                        // k-contiguous operand then reloads slot q right away;
+                        // a transposed store reads all four slots, so that
+                        // operand reloads them in k-group 1.
                         if (g == 0) {
-                            store_slot<AKC, Vec>(st_a, a_st, ra[s], s);
-                            store_slot<BKC, Vec>(st_b, b_st, rb[s], s);
-                            ra[s] = la.load(sa, kt + 2, s);
-                            rb[s] = lb.load(sb, kt + 2, s);
+                            store_slot<AKC, Vec>(st_a, a_st, ra, s);
+                            store_slot<BKC, Vec>(st_b, b_st, rb, s);
                         }
+                        if (g == (AKC ? 0 : 1)) ra[s] = la.load(sa, kt + 2, s);
+                        if (g == (BKC ? 0 : 1)) rb[s] = lb.load(sb, kt + 2, s);
                         if (g + 1 < BK / 8) {
-                            read_part<AKC>(as, wm, g + 1, lane, s, 0, fa[cb ^ 1]);
-                            read_part<BKC>(bs, wn, g + 1, lane, s, 2, fb[cb ^ 1]);
+                            read_part(as, wm, g + 1, lane, s, 0, fa[cb ^ 1]);
+                            read_part(bs, wn, g + 1, lane, s, 2, fb[cb ^ 1]);
                         } else {
-                            read_part<AKC>(as_next, wm, 0, lane, s, 0, fa[cb ^ 1]);
-                            read_part<BKC>(bs_next, wn, 0, lane, s, 2, fb[cb ^ 1]);
+                            read_part(as_next, wm, 0, lane, s, 0, fa[cb ^ 1]);
+                            read_part(bs_next, wn, 0, lane, s, 2, fb[cb ^ 1]);
                         }
 #pragma unroll
                         for (int i = 0; i < 2; ++i)

@@ -1,6 +1,6 @@
 """ORACLE build recipe — test infrastructure only.
 
-Builds two checkers:
+Builds the two CPU oracles:
   * oracle/liboracle.so  — the C restatement (vc_oracle.c) of the reference's
     CPU kernels, with gcc.
   * oracle/_ref/libvc_ref.so — the reference VectorCore C++ library compiled

@@ -1,6 +1,6 @@
 """ORACLE — test infrastructure only.
 
-ctypes wrappers over the two CPU checkers:
+ctypes wrappers over the two CPU oracles:
   * ``liboracle.so`` — the C restatement of the reference CPU kernels
     (vc_oracle.c), exposed as the functions in this module;
   * ``_ref/libvc_ref.so`` — the reference library built from its own sources

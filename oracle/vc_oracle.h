@@ -3,7 +3,7 @@
  *
  * A plain-C restatement of VectorCore's CPU kernels (the reference algorithm
  * for the backward-pass hot path). Only tests/, __graft_entry__.smoke() and
- * bench.py's cpu_baseline leg may load it, and only as the checker. The
+ * bench.py's cpu_baseline leg may load it, and only to check or time. The
  * product (vectorcore_amd) never links or calls it.
  *
  * Every function restates one reference routine and keeps its arithmetic

@@ -227,6 +227,19 @@ def test_cross_entropy_value_gradient_and_errors(device):
     assert np.isclose(vc.cross_entropy(T(np.zeros((3, 2)), device), np.array([0, 1, 1])).item(), np.log(2))
 
 
+def test_cross_entropy_with_changing_targets(device):
+    """The device keeps the last targets; a new vector replaces them."""
+    rng = np.random.default_rng(9)
+    logits = (rng.normal(size=(40, 7)) * 2).astype(np.float32)
+    a, b = rng.integers(0, 7, 40), rng.integers(0, 7, 40)
+    t = vc.Tensor(logits, device=device)
+    got = [vc.cross_entropy(t, tg).item() for tg in (a, b, a, a)]
+    cpu = vc.Tensor(logits)
+    want = [vc.cross_entropy(cpu, tg).item() for tg in (a, b, a, a)]
+    np.testing.assert_allclose(got, want, rtol=1e-6)
+    assert got[0] == got[2] == got[3] and got[0] != got[1]
+
+
 def test_cross_entropy_matches_torch(device):
     torch = pytest.importorskip("torch")
     rng = np.random.default_rng(6)

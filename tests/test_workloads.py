@@ -290,3 +290,28 @@ def test_mlp_full_size_step_against_float64_and_pool_reuse():
     # backward: every parameter gradient against float64 on the same forward
     for i, (g, r) in enumerate(zip(grads, mlp_backward_float64(m, zs_dev))):
         np.testing.assert_allclose(g, r, rtol=1e-4, atol=1e-5 * np.abs(r).max(), err_msg=f"parameter {i}")
+
+
+def test_mlp_train_steps_are_bitwise_reproducible():
+    """No atomics and shape-fixed partitions: the same steps from the same
+    start give the same losses and parameters, bit for bit (the split-K
+    products, the ReLU fold and the column sums included)."""
+    m = W.mlp(batch=1024, dims=(256, 2048, 512, 100))
+
+    def run():
+        params = build_mlp(m["weights"], m["biases"])
+        x = H(m["x"])
+        losses = []
+        for _ in range(3):
+            loss = vc.cross_entropy(mlp_logits(params, x), m["targets"])
+            loss.backward()
+            vc.sgd_step(params, 0.05)
+            vc.zero_grad(params)
+            losses.append(loss.item())
+        return losses, [p.numpy() for p in params]
+
+    l1, p1 = run()
+    l2, p2 = run()
+    assert l1 == l2 and l1[-1] < l1[0]
+    for a, b in zip(p1, p2):
+        np.testing.assert_array_equal(a, b)

@@ -365,12 +365,33 @@ std::pair<std::shared_ptr<Storage>, std::shared_ptr<Storage>> HipBackend::divide
     return {ga, gb};
 }
 
+namespace {
+// The last class-index vector uploaded. Device copies of targets are never
+// written, so a loss over the same targets as the previous one (a fixed
+// batch) reuses that buffer instead of copying it again. Never destroyed: it
+// must not release device memory after the HIP runtime has shut down.
+struct TargetsCache {
+    std::mutex mu;
+    std::vector<std::int32_t> host;
+    std::shared_ptr<Storage> device;
+};
+TargetsCache& targets_cache() {
+    static auto* cache = new TargetsCache();
+    return *cache;
+}
+}  // namespace
+
 std::shared_ptr<Storage> HipBackend::upload_targets(const std::vector<std::size_t>& targets) {
     require(*this);
     std::vector<std::int32_t> t(targets.size());
     for (std::size_t i = 0; i < targets.size(); ++i) t[i] = static_cast<std::int32_t>(targets[i]);
+    TargetsCache& cache = targets_cache();
+    std::lock_guard<std::mutex> lock(cache.mu);
+    if (cache.device && cache.host == t) return cache.device;
     auto out = fresh(targets.size());  // int32 and float have the same width
     if (!t.empty()) check(vc_hip_upload(out->ptr(), t.data(), t.size() * sizeof(std::int32_t)), "HIP upload failed");
+    cache.host = std::move(t);
+    cache.device = out;
     return out;
 }
 

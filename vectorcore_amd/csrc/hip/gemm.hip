@@ -198,10 +198,12 @@ template <bool TA, bool TB, bool Vec>
 __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmArgs p) {
     // Two LDS stages. Step kt multiplies out of stage cur while its first k-group
     // also stores slice kt + 1 (in registers since step kt - 1) into the other
-    // stage and issues the global loads of slice kt + 2. Fragments are read one
-    // k-group ahead; after the third group's MFMAs one barrier makes stage
-    // cur ^ 1 complete and stage cur free, and the fourth group's MFMAs overlap
-    // the reads of the next step's first group.
+    // stage and issues the global loads of slice kt + 2 (an m/n-contiguous
+    // operand in the second k-group, after its transposed stores have read all
+    // four slots). Fragments are read one k-group ahead; after the third
+    // group's MFMAs one barrier makes stage cur ^ 1 complete and stage cur
+    // free, and the fourth group's MFMAs overlap the reads of the next step's
+    // first group.
     __shared__ __attribute__((aligned(16))) float As[2][kLdsTile];
     __shared__ __attribute__((aligned(16))) float Bs[2][kLdsTile];
     constexpr bool AKC = !TA;  // A contiguous along k

@@ -111,6 +111,14 @@ int vc_hip_binary_scalar(const float* a, size_t count, float s, int scalar_first
 int vc_hip_unary(const float* in, float* out, size_t count, int op);
 /* MetalBackend::axpy_inplace (metal_backend.hpp:53-54): target += alpha * source. */
 int vc_hip_axpy(float* target, const float* source, size_t count, float alpha);
+/* vc_hip_axpy over a list of tensors: targets[k][i] += alpha * sources[k][i]
+ * for i < counts[k], in as few launches as the list allows (one per 16 aligned
+ * tensors). A target must not overlap another entry's target or source. The
+ * same bits as calling vc_hip_axpy once per tensor. No counterpart in the
+ * reference: it serves nn::sgd_step (src/nn.cpp:55-76), which applies
+ * axpy_inplace (metal_backend.hpp:53-54) to each parameter in turn. */
+int vc_hip_axpy_batch(float* const* targets, const float* const* sources, const size_t* counts, size_t tensors,
+                      float alpha);
 
 /* Fused activation gradients (one pass each; same-shape contiguous operands).
  * relu:    out = grad * (input > 0 ? 1 : 0)         (src/ops.cpp:398-401)

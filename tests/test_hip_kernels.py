@@ -218,6 +218,33 @@ def test_axpy_matches_sgd_bitexact():
     np.testing.assert_array_equal(dp.numpy(), expected)
 
 
+def test_axpy_batch_matches_per_tensor_sgd_bitexact():
+    # 21 tensors: more than one launch's list, empty and sub-vector sizes,
+    # ragged tails, and two views at a 4-byte offset (the unaligned path).
+    rng = np.random.default_rng(11)
+    sizes_ = [25_001, 0, 1, 3, 4, 5, 4097, 128, 77, 1 << 16, 9, 2, 6, 31, 64, 1000, 17, 8, 12345, 3, 513]
+    params = [rng.standard_normal(s).astype(np.float32) for s in sizes_]
+    grads = [rng.standard_normal(s).astype(np.float32) for s in sizes_]
+    bufs = []
+    targets, sources = [], []
+    for i, (p, g) in enumerate(zip(params, grads)):
+        shift = 1 if i in (4, 17) else 0  # a float into a larger buffer: not 16-byte aligned
+        dp = C.Buffer.of(np.concatenate([np.zeros(shift, np.float32), p]))
+        dg = C.Buffer.of(np.concatenate([np.zeros(shift, np.float32), g]))
+        bufs.append((dp, dg, shift))
+        targets.append(dp.ptr + 4 * shift)
+        sources.append(dg.ptr + 4 * shift)
+    n = len(sizes_)
+    C.check(C.lib().vc_hip_axpy_batch((ctypes.c_void_p * n)(*targets), (ctypes.c_void_p * n)(*sources), C.sizes(sizes_),
+                                      n, ctypes.c_float(-0.05)))
+    for (dp, _, shift), p, g in zip(bufs, params, grads):
+        expected = p.copy()
+        K.sgd_(expected, g, 0.05)
+        got = dp.numpy()[shift:]
+        np.testing.assert_array_equal(got, expected)
+    C.check(C.lib().vc_hip_axpy_batch(None, None, None, 0, ctypes.c_float(1.0)))
+
+
 def reduce_axis_dev(x, axis, op):
     _, outer, length, inner, _, removed = K.split_axis(x.shape, axis)
     dx, dy = C.Buffer.of(x), C.Buffer(removed)

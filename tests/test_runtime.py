@@ -614,6 +614,35 @@ def test_hip_synchronize_and_sgd_matches_cpu():
 
 
 @hip_only
+def test_hip_sgd_over_many_parameters_matches_one_at_a_time():
+    # sgd_step batches hip parameters into list launches; a parameter listed
+    # twice must still be stepped twice, in order, like the one-at-a-time loop.
+    rng = np.random.default_rng(3)
+    shapes = [(int(rng.integers(1, 300)),) for _ in range(19)] + [(64, 33), (5,)]
+    data = [rng.normal(size=s).astype(np.float32) for s in shapes]
+    coef = [rng.normal(size=s).astype(np.float32) for s in shapes]
+
+    def stepped(batched):
+        ps = [vc.Tensor(d, requires_grad=True, device="hip") for d in data]
+        loss = None
+        for p, c in zip(ps, coef):
+            term = (p * vc.Tensor(c, device="hip")).sum()
+            loss = term if loss is None else loss + term
+        loss.backward()
+        order = ps + [ps[3], ps[20]]
+        if batched:
+            vc.sgd_step(order, 0.25)
+        else:
+            for p in order:
+                vc.sgd_step([p], 0.25)
+        return [npy(p) for p in ps]
+
+    for got, want in zip(stepped(True), stepped(False)):
+        np.testing.assert_array_equal(got, want)
+    np.testing.assert_allclose(stepped(True)[3], data[3] - 0.5 * coef[3], rtol=1e-6, atol=1e-6)
+
+
+@hip_only
 def test_hip_gemm_kernel_reported():
     assert vc.hip_gemm_kernel() in ("mfma", "simple")
     assert "gfx950" in vc.hip_device_name()

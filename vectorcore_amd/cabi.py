@@ -44,6 +44,7 @@ _SIGNATURES = {
     "vc_hip_binary_scalar": ([_vp, _sz, _f, _i, _vp, _i], _i),
     "vc_hip_unary": ([_vp, _vp, _sz, _i], _i),
     "vc_hip_axpy": ([_vp, _vp, _sz, _f], _i),
+    "vc_hip_axpy_batch": ([ctypes.POINTER(_vp), ctypes.POINTER(_vp), _szp, _sz, _f], _i),
     "vc_hip_relu_backward": ([_vp, _vp, _vp, _sz], _i),
     "vc_hip_sigmoid_backward": ([_vp, _vp, _vp, _sz], _i),
     "vc_hip_exp_backward": ([_vp, _vp, _vp, _sz], _i),

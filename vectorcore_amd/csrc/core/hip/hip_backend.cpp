@@ -316,6 +316,25 @@ void HipBackend::axpy_inplace(Storage& target, std::size_t target_offset, const 
     check(vc_hip_axpy(t.ptr() + target_offset, dptr(source, source_offset), count, alpha), "HIP axpy failed");
 }
 
+void HipBackend::axpy_batch(const std::vector<AxpyItem>& items, float alpha) {
+    require(*this);
+    std::vector<float*> targets;
+    std::vector<const float*> sources;
+    std::vector<std::size_t> counts;
+    for (const AxpyItem& it : items) {
+        if (it.target_offset + it.count > it.target->size() || it.source_offset + it.count > it.source->size())
+            throw std::out_of_range("HIP axpy exceeds storage");
+        auto& t = as_hip(*it.target);
+        t.written_on_device();
+        if (it.count == 0) continue;
+        targets.push_back(t.ptr() + it.target_offset);
+        sources.push_back(dptr(*it.source, it.source_offset));
+        counts.push_back(it.count);
+    }
+    if (targets.empty()) return;
+    check(vc_hip_axpy_batch(targets.data(), sources.data(), counts.data(), targets.size(), alpha), "HIP axpy failed");
+}
+
 void HipBackend::synchronize() {
     if (!available()) return;
     check(vc_hip_synchronize(), "HIP command failed");

@@ -63,6 +63,17 @@ public:
                                                         std::size_t outer, std::size_t length, std::size_t inner);
     void axpy_inplace(Storage& target, std::size_t target_offset, const Storage& source, std::size_t source_offset,
                       std::size_t count, float alpha);
+    // axpy_inplace for several (target, source) pairs in one pass. A target
+    // must not overlap another pair's target or source; the result is then the
+    // same bits as one axpy_inplace per pair.
+    struct AxpyItem {
+        Storage* target;
+        std::size_t target_offset;
+        const Storage* source;
+        std::size_t source_offset;
+        std::size_t count;
+    };
+    void axpy_batch(const std::vector<AxpyItem>& items, float alpha);
     void synchronize();
 
     // --- fused kernels used by the hip arm of the backward rules ---

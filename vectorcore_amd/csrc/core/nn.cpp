@@ -5,6 +5,7 @@
 #include "vectorcore/hip_backend.hpp"
 #include "vectorcore/ops.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <stdexcept>
 #include <string>
@@ -83,23 +84,45 @@ Tensor cross_entropy(const Tensor& logits, const std::vector<std::size_t>& targe
 
 void sgd_step(const std::vector<Tensor*>& parameters, float learning_rate) {
     NoGradGuard guard;
+    // hip parameters are updated in batches (one launch for up to 16), in
+    // parameter order: a batch is flushed before anything that the reference's
+    // one-at-a-time loop would order after it (an error, a cpu parameter, a
+    // parameter sharing a batched storage).
+    std::vector<HipBackend::AxpyItem> batch;
+    std::vector<Storage*> touched;        // targets in the batch
+    std::vector<const Storage*> read;     // sources in the batch
+    const auto contains = [](const auto& v, const Storage* s) { return std::find(v.begin(), v.end(), s) != v.end(); };
+    const auto flush = [&] {
+        if (batch.empty()) return;
+        HipBackend::instance().axpy_batch(batch, -learning_rate);
+        for (Storage* s : touched) s->bump_version();  // an in-place update, like mutable_data()
+        batch.clear();
+        touched.clear();
+        read.clear();
+    };
     for (Tensor* p : parameters) {
         if (!p || !p->has_grad()) continue;
         const Tensor g = p->grad();
-        if (g.shape() != p->shape() || g.device() != p->device())
+        if (g.shape() != p->shape() || g.device() != p->device()) {
+            flush();
             throw std::invalid_argument("parameter gradient shape or device does not match");
+        }
         if (p->device() == Device::hip()) {
-            auto& storage = *p->impl()->storage;
-            HipBackend::instance().axpy_inplace(storage, p->impl()->offset, *g.impl()->storage, g.impl()->offset,
-                                                p->numel(), -learning_rate);
-            storage.bump_version();  // an in-place update, like mutable_data()
+            Storage* storage = p->impl()->storage.get();
+            const Storage* source = g.impl()->storage.get();
+            if (contains(touched, storage) || contains(read, storage) || contains(touched, source)) flush();
+            batch.push_back({storage, p->impl()->offset, source, g.impl()->offset, p->numel()});
+            touched.push_back(storage);
+            read.push_back(source);
             continue;
         }
+        flush();
         if (p->device() != Device::cpu()) throw std::runtime_error("Metal is unavailable: VectorCore was built without Apple Metal");
         const auto gv = g.to_vector();
         float* values = p->mutable_data();
         for (std::size_t i = 0; i < p->numel(); ++i) values[i] -= learning_rate * gv[i];
     }
+    flush();
 }
 
 void zero_grad(const std::vector<Tensor*>& parameters) {

@@ -119,6 +119,38 @@ __global__ __launch_bounds__(kBlock) void map2_kernel(const float* __restrict__ 
     if (t < tail) y[4 * n4 + t] = f(a[4 * n4 + t], b[4 * n4 + t]);
 }
 
+// SGD over a list of parameters in one launch: t_k += alpha * s_k for every
+// tensor k, as the per-tensor axpy computes it. The tensors are laid end to
+// end in 16-byte chunks (first[k] = chunks before tensor k); a thread finds its
+// tensor by a short scan. Each tensor's last chunk may be partial.
+constexpr int kAxpyList = 16;
+struct AxpyList {
+    float* t[kAxpyList];
+    const float* s[kAxpyList];
+    int64_t count[kAxpyList];
+    int64_t first[kAxpyList + 1];
+    int n;
+    float alpha;
+};
+
+__global__ __launch_bounds__(kBlock) void axpy_list_kernel(AxpyList L) {
+    const int64_t total = L.first[L.n];
+    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    const AxpyOp f{L.alpha};
+    for (int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; c < total; c += stride) {
+        int k = 0;
+        while (c >= L.first[k + 1]) ++k;
+        const int64_t e = (c - L.first[k]) * 4;
+        float* t = L.t[k] + e;
+        const float* src = L.s[k] + e;
+        if (e + 4 <= L.count[k]) {
+            st4(t, apply4(f, ld4(t), ld4(src)));
+        } else {
+            for (int64_t i = 0; e + i < L.count[k]; ++i) t[i] = f(t[i], src[i]);
+        }
+    }
+}
+
 // Scalar fallbacks for buffers that are not 16-byte aligned.
 template <class F>
 __global__ __launch_bounds__(kBlock) void map1_scalar_kernel(const float* __restrict__ x, float* __restrict__ y, size_t n, F f) {
@@ -371,6 +403,41 @@ int vc_hip_unary(const float* in, float* out, size_t count, int op) {
 
 int vc_hip_axpy(float* target, const float* source, size_t count, float alpha) {
     return guard([&] { launch_map2("axpy", target, source, target, count, AxpyOp{alpha}, 12.0); });
+}
+
+int vc_hip_axpy_batch(float* const* targets, const float* const* sources, const size_t* counts, size_t tensors,
+                      float alpha) {
+    return guard([&] {
+        Device& d = require_device();
+        if (tensors > 0 && (!targets || !sources || !counts)) fail(VC_HIP_ERR_INVALID_ARGUMENT, "axpy_batch: null list");
+        size_t i = 0;
+        while (i < tensors) {
+            AxpyList L{};
+            double bytes = 0.0;
+            // Up to kAxpyList 16-byte-aligned tensors per launch; any other
+            // tensor goes through the single-tensor kernel on its own.
+            for (; i < tensors && L.n < kAxpyList; ++i) {
+                if (counts[i] == 0) continue;
+                if (!targets[i] || !sources[i]) fail(VC_HIP_ERR_INVALID_ARGUMENT, "axpy_batch: null buffer");
+                if (!aligned16(targets[i]) || !aligned16(sources[i])) {
+                    launch_map2("axpy", targets[i], sources[i], targets[i], counts[i], AxpyOp{alpha}, 12.0);
+                    continue;
+                }
+                L.t[L.n] = targets[i];
+                L.s[L.n] = sources[i];
+                L.count[L.n] = int64_t(counts[i]);
+                L.first[L.n + 1] = L.first[L.n] + int64_t((counts[i] + 3) / 4);
+                bytes += 12.0 * double(counts[i]);
+                ++L.n;
+            }
+            if (L.n == 0) continue;
+            L.alpha = alpha;
+            Profiled p("axpy", 0.0, bytes);
+            launch(axpy_list_kernel, dim3(stream_grid(size_t(L.first[L.n]))), dim3(kBlock), 0, d.stream, L);
+            after_launch("axpy");
+            p.done();
+        }
+    });
 }
 
 int vc_hip_relu_backward(const float* grad, const float* input, float* out, size_t count) {

@@ -111,14 +111,15 @@ int vc_hip_binary_scalar(const float* a, size_t count, float s, int scalar_first
 int vc_hip_unary(const float* in, float* out, size_t count, int op);
 /* MetalBackend::axpy_inplace (metal_backend.hpp:53-54): target += alpha * source. */
 int vc_hip_axpy(float* target, const float* source, size_t count, float alpha);
-/* vc_hip_axpy over a list of tensors: targets[k][i] += alpha * sources[k][i]
- * for i < counts[k], in as few launches as the list allows (one per 16 aligned
- * tensors). A target must not overlap another entry's target or source. The
- * same bits as calling vc_hip_axpy once per tensor. No counterpart in the
- * reference: it serves nn::sgd_step (src/nn.cpp:55-76), which applies
- * axpy_inplace (metal_backend.hpp:53-54) to each parameter in turn. */
-int vc_hip_axpy_batch(float* const* targets, const float* const* sources, const size_t* counts, size_t tensors,
-                      float alpha);
+/* vc_hip_axpy over a list of tensors: outputs[k][i] = targets[k][i] +
+ * alpha * sources[k][i] for i < counts[k] (outputs[k] == targets[k] updates in
+ * place), in as few launches as the list allows (one per 16 aligned tensors).
+ * An output must not overlap another entry's buffers. The same bits as calling
+ * vc_hip_axpy once per tensor. No counterpart in the reference: it serves
+ * nn::sgd_step (src/nn.cpp:55-76), which applies axpy_inplace
+ * (metal_backend.hpp:53-54) to each parameter in turn. */
+int vc_hip_axpy_batch(float* const* outputs, const float* const* targets, const float* const* sources,
+                      const size_t* counts, size_t tensors, float alpha);
 
 /* Fused activation gradients (one pass each; same-shape contiguous operands).
  * relu:    out = grad * (input > 0 ? 1 : 0)         (src/ops.cpp:398-401)
@@ -152,6 +153,16 @@ int vc_hip_matmul(const float* a, const float* b, float* c, size_t m, size_t k, 
 int vc_hip_matmul_relu_mask(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
                             const size_t* a_offsets, const size_t* b_offsets, size_t batch, int trans_a, int trans_b,
                             const float* relu_input);
+/* A forward layer in one kernel: c = a @ b (+ bias[column]) (then ReLU),
+ * a [m][k], b [k][n], bias [n] or null, all contiguous; relu nonzero applies
+ * x > 0 ? x : 0 after the bias. The same bits as vc_hip_matmul, then the
+ * row-broadcast vc_hip_binary add, then vc_hip_unary relu. k must be > 0. No
+ * counterpart in the reference: it fuses the add (src/ops.cpp:98-109, as
+ * nn::Linear composes it, src/nn.cpp:23) and the ReLU forward
+ * (src/ops.cpp:395-397) into the product (src/ops.cpp:244-249) when the
+ * runtime finds those ops applied to a product not yet computed. */
+int vc_hip_matmul_bias_relu(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                            const float* bias, int relu);
 
 /* Batch-reduced product for gradients of a batch-broadcast operand
  * (src/ops.cpp:252-260 followed by sum_to_shape over the batch):

@@ -110,6 +110,28 @@ def test_gemm_relu_mask_is_gemm_then_relu_backward_bitexact():
             assert (fused.numpy() == 0).any() and (fused.numpy() != 0).any()
 
 
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (300, 513, 257), (129, 64, 4100), (64, 4096, 64), (256, 2048, 384)])
+def test_matmul_bias_relu_is_product_then_add_then_relu_bitexact(m, k, n):
+    # The fused epilogue against the unfused product followed by the row add
+    # and ReLU in fp32 (x > 0 ? x : 0). (64, 4096, 64) splits K, so the
+    # epilogue runs in the split combine.
+    rng = np.random.default_rng(m + k + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    product = run_gemm(a, b, m, k, n, False, False)[0]
+    np.testing.assert_allclose(product, K.matmul2d(a, b), rtol=1e-4, atol=1e-4 * np.sqrt(k))
+    da, db, dbias = C.Buffer.of(a), C.Buffer.of(b), C.Buffer.of(bias)
+    for with_bias, relu in [(True, True), (True, False), (False, True)]:
+        dc = C.Buffer((m, n))
+        C.check(C.lib().vc_hip_matmul_bias_relu(da.ptr, db.ptr, dc.ptr, m, k, n, dbias.ptr if with_bias else None,
+                                                int(relu)))
+        expected = product + bias if with_bias else product.copy()
+        if relu:
+            expected = np.where(expected > 0, expected, np.float32(0))
+        np.testing.assert_array_equal(dc.numpy(), expected)
+
+
 def test_gemm_batch_reduce_matches_summed_products():
     """dB of a batch-broadcast B: sum_z A[z]^T dC[z] in one launch."""
     bm = W.bmm(batch=3, m=96, k=80, n=72, seed=1)
@@ -225,24 +247,29 @@ def test_axpy_batch_matches_per_tensor_sgd_bitexact():
     sizes_ = [25_001, 0, 1, 3, 4, 5, 4097, 128, 77, 1 << 16, 9, 2, 6, 31, 64, 1000, 17, 8, 12345, 3, 513]
     params = [rng.standard_normal(s).astype(np.float32) for s in sizes_]
     grads = [rng.standard_normal(s).astype(np.float32) for s in sizes_]
+    # Every third entry writes a separate output buffer and leaves its target alone.
     bufs = []
-    targets, sources = [], []
+    outputs, targets, sources = [], [], []
     for i, (p, g) in enumerate(zip(params, grads)):
         shift = 1 if i in (4, 17) else 0  # a float into a larger buffer: not 16-byte aligned
         dp = C.Buffer.of(np.concatenate([np.zeros(shift, np.float32), p]))
         dg = C.Buffer.of(np.concatenate([np.zeros(shift, np.float32), g]))
-        bufs.append((dp, dg, shift))
+        do = C.Buffer((shift + p.size,)) if i % 3 == 2 else dp
+        bufs.append((dp, do, dg, shift))  # every buffer stays alive until the checks
+        outputs.append(do.ptr + 4 * shift)
         targets.append(dp.ptr + 4 * shift)
         sources.append(dg.ptr + 4 * shift)
     n = len(sizes_)
-    C.check(C.lib().vc_hip_axpy_batch((ctypes.c_void_p * n)(*targets), (ctypes.c_void_p * n)(*sources), C.sizes(sizes_),
-                                      n, ctypes.c_float(-0.05)))
-    for (dp, _, shift), p, g in zip(bufs, params, grads):
+    ptrs = ctypes.c_void_p * n
+    C.check(C.lib().vc_hip_axpy_batch(ptrs(*outputs), ptrs(*targets), ptrs(*sources), C.sizes(sizes_), n,
+                                      ctypes.c_float(-0.05)))
+    for (dp, do, _, shift), p, g in zip(bufs, params, grads):
         expected = p.copy()
         K.sgd_(expected, g, 0.05)
-        got = dp.numpy()[shift:]
-        np.testing.assert_array_equal(got, expected)
-    C.check(C.lib().vc_hip_axpy_batch(None, None, None, 0, ctypes.c_float(1.0)))
+        np.testing.assert_array_equal(do.numpy()[shift:], expected)
+        if do is not dp:
+            np.testing.assert_array_equal(dp.numpy()[shift:], p)
+    C.check(C.lib().vc_hip_axpy_batch(None, None, None, None, 0, ctypes.c_float(1.0)))
 
 
 def reduce_axis_dev(x, axis, op):

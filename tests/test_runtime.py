@@ -359,6 +359,132 @@ def test_relu_fold_keeps_the_version_check(device):
         loss.backward()
 
 
+# --- deferred forward products (hip) --------------------------------------------------
+# A 2-D product on hip is computed when its storage is first read, so that a
+# row-bias add and a ReLU applied to it run in the product's epilogue. Every
+# observable value must be the bits of eager execution.
+
+
+def _eager_then_deferred(fn):
+    previous = vc.hip_defer_products(False)
+    try:
+        eager = fn()
+    finally:
+        vc.hip_defer_products(previous)
+    vc.hip_defer_products(True)
+    try:
+        return eager, fn()
+    finally:
+        vc.hip_defer_products(previous)
+
+
+def _assert_same_bits(eager, deferred):
+    assert len(eager) == len(deferred)
+    for i, (e, d) in enumerate(zip(eager, deferred)):
+        np.testing.assert_array_equal(np.asarray(d), np.asarray(e), err_msg=f"value {i}")
+
+
+@hip_only
+def test_deferred_layers_give_the_eager_bits():
+    rng = np.random.default_rng(5)
+    xs = rng.standard_normal((300, 70)).astype(np.float32)
+    ws = [(rng.standard_normal((70, 130)) * 0.2).astype(np.float32),
+          (rng.standard_normal((130, 33)) * 0.2).astype(np.float32)]
+    bs = [(rng.standard_normal(130) * 0.1).astype(np.float32), (rng.standard_normal((1, 33)) * 0.1).astype(np.float32)]
+    targets = [i % 33 for i in range(300)]
+
+    def run():
+        x = vc.Tensor(xs, device="hip")
+        w1, w2 = (vc.Tensor(w, requires_grad=True, device="hip") for w in ws)
+        b1, b2 = (vc.Tensor(b, requires_grad=True, device="hip") for b in bs)
+        pre = x @ w1 + b1
+        h = pre.relu()
+        logits = b2 + h @ w2  # the bias as the left operand
+        loss = vc.cross_entropy(logits, targets)
+        loss.backward()
+        out = [loss.item()] + [npy(p.grad) for p in (w1, b1, w2, b2)]
+        vc.sgd_step([w1, b1, w2, b2], 0.1)
+        # read after the update: the values of the forward pass
+        out += [npy(pre), npy(h), npy(logits)] + [npy(p) for p in (w1, b1, w2, b2)]
+        return out
+
+    _assert_same_bits(*_eager_then_deferred(run))
+
+
+@hip_only
+def test_deferred_product_read_after_its_operands_change():
+    rng = np.random.default_rng(6)
+    xs = rng.standard_normal((40, 24)).astype(np.float32)
+    w0 = rng.standard_normal((24, 36)).astype(np.float32)
+    b0 = rng.standard_normal(36).astype(np.float32)
+
+    def run():
+        x = vc.Tensor(xs, device="hip")
+        w = vc.Tensor(w0, requires_grad=True, device="hip")
+        b = vc.Tensor(b0, requires_grad=True, device="hip")
+        p1 = x @ w
+        q1 = (p1 + b).relu()
+        ((w * 1.0).sum() + (b * 1.0).sum()).backward()
+        vc.sgd_step([w, b], 0.5)  # w -= 0.5, b -= 0.5
+        p2 = x @ w
+        q2 = p2 + b
+        vc.sgd_step([w, b], 0.5)  # a second update while p2 and q2 are still pending
+        p3 = (x @ w).relu()
+        return [npy(q1), npy(p1), npy(q2), npy(p2), npy(p3), npy(w), npy(b)]
+
+    eager, deferred = _eager_then_deferred(run)
+    _assert_same_bits(eager, deferred)
+    tol = dict(rtol=1e-4, atol=1e-4 * np.sqrt(24))
+    np.testing.assert_allclose(deferred[1], xs.astype(np.float64) @ w0, **tol)
+    np.testing.assert_allclose(deferred[0], np.maximum(xs.astype(np.float64) @ w0 + b0, 0), **tol)
+    np.testing.assert_allclose(deferred[2], xs.astype(np.float64) @ (w0 - 0.5) + (b0 - 0.5), **tol)
+    np.testing.assert_allclose(deferred[4], np.maximum(xs.astype(np.float64) @ (w0 - 1.0), 0), **tol)
+
+
+@hip_only
+def test_deferred_product_shared_reshaped_and_as_a_bias():
+    rng = np.random.default_rng(8)
+    xs, ws = rng.standard_normal((17, 9)).astype(np.float32), rng.standard_normal((9, 21)).astype(np.float32)
+    us, vs = rng.standard_normal((1, 5)).astype(np.float32), rng.standard_normal((5, 21)).astype(np.float32)
+
+    def run():
+        x, w = vc.Tensor(xs, device="hip"), vc.Tensor(ws, requires_grad=True, device="hip")
+        u, v = vc.Tensor(us, device="hip"), vc.Tensor(vs, requires_grad=True, device="hip")
+        h = x @ w
+        bias = u @ v  # [1, 21], itself a deferred product
+        fused = (h + bias).relu()
+        doubled = h * 2.0  # h is also read directly
+        flat = (x @ w).reshape([17 * 21]).relu()  # elementwise, so the ReLU of a reshaped product still fuses
+        (fused.sum() + doubled.sum() + flat.sum()).backward()
+        return [npy(fused), npy(doubled), npy(flat), npy(w.grad), npy(v.grad)]
+
+    _assert_same_bits(*_eager_then_deferred(run))
+
+
+@hip_only
+def test_relu_rule_falls_back_to_its_input_when_the_output_changes():
+    rng = np.random.default_rng(9)
+    xs, ws = rng.standard_normal((6, 5)).astype(np.float32), rng.standard_normal((5, 4)).astype(np.float32)
+
+    def run(device):
+        x = vc.Tensor(xs, requires_grad=True, device=device)
+        w = vc.Tensor(ws, device=device)
+        y = (x @ w).relu()
+        loss = y.sum()
+        ys = y.detach()
+        ys.requires_grad = True
+        (ys * -3.0).sum().backward()
+        vc.sgd_step([ys], 1.0)  # rewrites the ReLU's output: every entry becomes >= 3
+        loss.backward()  # the mask must still be [x @ w > 0]
+        return [npy(x.grad), npy(y)]
+
+    got = run("hip")
+    np.testing.assert_allclose(got[0], run("cpu")[0], rtol=1e-5, atol=1e-5)
+    assert (got[1] >= 3.0).all()
+    mask = (xs.astype(np.float64) @ ws > 0).astype(np.float64)
+    np.testing.assert_allclose(got[0], mask @ ws.T, rtol=1e-5, atol=1e-5)
+
+
 # --- finite-difference gradcheck (test_autograd_correctness.py:47-143) ----------------
 
 

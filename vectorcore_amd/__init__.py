@@ -4,7 +4,7 @@ The module surface is the reference's `vectorcore` Python module
 (python/bindings.cpp): ``import vectorcore_amd as vc`` then ``vc.Tensor``,
 ``vc.Linear``, ``vc.cross_entropy``, ``vc.sgd_step``, ... with ``device="hip"``
 accepted wherever a device is. The native extension (and libvc_hip.so, which
-it links) must be built in-tree: ``python -m vectorcore_amd.build``.
+it links) must be built in-tree: ``python vectorcore_amd/build.py``.
 """
 
 from ._vectorcore import (  # noqa: F401
@@ -12,6 +12,7 @@ from ._vectorcore import (  # noqa: F401
     Tensor,
     cross_entropy,
     hip_available,
+    hip_defer_products,
     hip_device_name,
     hip_gemm_kernel,
     hip_pool_stats,

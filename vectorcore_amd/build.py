@@ -4,7 +4,7 @@
   _vectorcore*.so  the C++20 tensor/autograd runtime and its pybind11 module,
                  linked against libvc_hip.so (rpath $ORIGIN)
 
-Run `python -m vectorcore_amd.build` (or __graft_entry__.build()). Every call
+Run `python vectorcore_amd/build.py` (or __graft_entry__.build()). Every call
 recompiles; objects go to vectorcore_amd/_build/, libraries next to this file.
 """
 

@@ -44,7 +44,7 @@ _SIGNATURES = {
     "vc_hip_binary_scalar": ([_vp, _sz, _f, _i, _vp, _i], _i),
     "vc_hip_unary": ([_vp, _vp, _sz, _i], _i),
     "vc_hip_axpy": ([_vp, _vp, _sz, _f], _i),
-    "vc_hip_axpy_batch": ([ctypes.POINTER(_vp), ctypes.POINTER(_vp), _szp, _sz, _f], _i),
+    "vc_hip_axpy_batch": ([ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp), _szp, _sz, _f], _i),
     "vc_hip_relu_backward": ([_vp, _vp, _vp, _sz], _i),
     "vc_hip_sigmoid_backward": ([_vp, _vp, _vp, _sz], _i),
     "vc_hip_exp_backward": ([_vp, _vp, _vp, _sz], _i),
@@ -52,6 +52,7 @@ _SIGNATURES = {
     "vc_hip_div_backward": ([_vp, _vp, _szp, _szp, _sz, _vp, _szp, _szp, _sz, _szp, _sz, _vp, _vp], _i),
     "vc_hip_matmul": ([_vp, _vp, _vp, _sz, _sz, _sz, _szp, _szp, _sz, _i, _i], _i),
     "vc_hip_matmul_relu_mask": ([_vp, _vp, _vp, _sz, _sz, _sz, _szp, _szp, _sz, _i, _i, _vp], _i),
+    "vc_hip_matmul_bias_relu": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp, _i], _i),
     "vc_hip_matmul_reduce": ([_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _i], _i),
     "vc_hip_transpose_last2": ([_vp, _vp, _sz, _sz, _sz], _i),
     "vc_hip_reduce_sum": ([_vp, _sz, _vp], _i),
@@ -83,7 +84,7 @@ def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
-            raise RuntimeError(f"{LIB_PATH} is not built; run python -m vectorcore_amd.build")
+            raise RuntimeError(f"{LIB_PATH} is not built; run python vectorcore_amd/build.py")
         handle = ctypes.CDLL(str(LIB_PATH))
         for name, (args, res) in _SIGNATURES.items():
             fn = getattr(handle, name)

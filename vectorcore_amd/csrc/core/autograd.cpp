@@ -39,6 +39,11 @@ Tensor SavedTensor::unpack() const {
     return tensor_;
 }
 
+std::optional<Tensor> SavedTensor::unpack_if_unchanged() const {
+    if (tensor_.version() != version_) return std::nullopt;
+    return tensor_;
+}
+
 void attach_grad_fn(Tensor& output, const std::vector<Tensor>& parents,
                     std::function<std::vector<Tensor>(const Tensor&)> backward) {
     if (!grad_enabled()) return;

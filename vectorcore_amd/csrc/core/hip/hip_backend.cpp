@@ -10,6 +10,9 @@
 
 #include "vc_hip.h"
 
+#include <algorithm>
+#include <atomic>
+#include <cstdlib>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -32,14 +35,46 @@ inline void check(int status, const char* what) {
     if (status != VC_HIP_OK) throw_status(status, what);
 }
 
-class HipStorage final : public Storage {
+// The state of every hip storage (buffer, host shadow, deferred product,
+// readers) is guarded by one recursive mutex: computing a deferred product
+// reads its operands, which may be deferred products themselves.
+std::recursive_mutex& state_mutex() {
+    static std::recursive_mutex mu;
+    return mu;
+}
+
+class HipStorage;
+
+// A forward product recorded but not launched yet:
+// C = A [m, k] @ B [k, n] (+ bias [n] on every row) (then ReLU), all contiguous.
+struct DeferredProduct {
+    std::shared_ptr<HipStorage> a, b, bias;
+    std::size_t a_offset = 0, b_offset = 0, bias_offset = 0;
+    std::size_t m = 0, k = 0, n = 0;
+    bool relu = false;
+
+    [[nodiscard]] bool reads(const HipStorage* s) const { return a.get() == s || b.get() == s || bias.get() == s; }
+    void replace(const HipStorage* s, const std::shared_ptr<HipStorage>& with) {
+        if (a.get() == s) a = with;
+        if (b.get() == s) b = with;
+        if (bias.get() == s) bias = with;
+    }
+};
+
+class HipStorage final : public Storage, public std::enable_shared_from_this<HipStorage> {
 public:
     // A fresh pooled buffer of `elements` floats (contents undefined).
-    explicit HipStorage(std::size_t elements) : elements_(elements) {
+    explicit HipStorage(std::size_t elements) : elements_(elements), shadow_valid_(false) {
         check(vc_hip_alloc(bytes(), &ptr_), "HIP allocation failed");
     }
     // A small tensor from host values: kept on the host until a kernel needs it.
-    HipStorage(const float* values, std::size_t elements) : elements_(elements), shadow_(values, values + elements) {}
+    HipStorage(const float* values, std::size_t elements)
+        : elements_(elements), shadow_(values, values + elements), shadow_valid_(true) {}
+    // A product computed on first use (see ptr()).
+    HipStorage(std::size_t elements, DeferredProduct product)
+        : elements_(elements), deferred_(std::make_unique<DeferredProduct>(std::move(product))), shadow_valid_(false) {}
+    // Takes over a pooled buffer that already holds this storage's contents.
+    HipStorage(std::size_t elements, void* buffer) : elements_(elements), ptr_(buffer), shadow_valid_(false) {}
 
     ~HipStorage() override {
         if (ptr_) (void)vc_hip_release(ptr_);
@@ -50,44 +85,94 @@ public:
     [[nodiscard]] Device device() const noexcept override { return Device::hip(); }
     [[nodiscard]] std::size_t size() const noexcept override { return elements_; }
 
+    // The device buffer, allocated, uploaded or computed (a deferred product)
+    // on first use.
     float* ptr() const {
-        std::lock_guard<std::mutex> lock(mu_);
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
         if (!ptr_) {
             check(vc_hip_alloc(bytes(), &ptr_), "HIP allocation failed");
             if (!shadow_.empty()) check(vc_hip_upload(ptr_, shadow_.data(), shadow_.size() * sizeof(float)), "HIP upload failed");
+        }
+        if (deferred_) {
+            const DeferredProduct& d = *deferred_;
+            check(vc_hip_matmul_bias_relu(d.a->ptr() + d.a_offset, d.b->ptr() + d.b_offset, static_cast<float*>(ptr_),
+                                          d.m, d.k, d.n, d.bias ? d.bias->ptr() + d.bias_offset : nullptr,
+                                          d.relu ? 1 : 0),
+                  "HIP matmul failed");
+            deferred_.reset();  // drops the operands
         }
         return static_cast<float*>(ptr_);
     }
 
     std::optional<float> host_scalar() const {
-        std::lock_guard<std::mutex> lock(mu_);
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
         if (elements_ == 1 && shadow_valid_ && shadow_.size() == 1) return shadow_[0];
         return std::nullopt;
     }
 
     // Host copy readable without the device (no synchronisation needed).
     bool host_copy(std::size_t offset, float* dst, std::size_t n) const {
-        std::lock_guard<std::mutex> lock(mu_);
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
         if (!shadow_valid_ || shadow_.empty()) return false;
         std::copy(shadow_.begin() + static_cast<std::ptrdiff_t>(offset),
                   shadow_.begin() + static_cast<std::ptrdiff_t>(offset + n), dst);
         return true;
     }
 
-    void written_on_device() {
+    // The deferred product this storage still has to compute, if any (a copy
+    // for building a product with a longer epilogue).
+    std::optional<DeferredProduct> pending() const {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        if (!deferred_) return std::nullopt;
+        return *deferred_;
+    }
+
+    // Records `reader` as a deferred product that reads this storage.
+    void add_reader(const std::shared_ptr<HipStorage>& reader) {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        readers_.erase(std::remove_if(readers_.begin(), readers_.end(), [](const auto& w) { return w.expired(); }),
+                       readers_.end());
+        readers_.push_back(reader);
+    }
+
+    // Before an in-place write of this storage. Deferred products that read it
+    // and have not run yet must still see the current contents: the current
+    // buffer moves to a new read-only storage that those products read from,
+    // and this storage continues with a fresh buffer. Returns the storage whose
+    // buffer holds the current contents (this one when nothing was deferred on
+    // it); the caller keeps it alive until the write is enqueued and writes
+    // its result into ptr().
+    std::shared_ptr<const HipStorage> before_write() {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
         (void)ptr();
-        std::lock_guard<std::mutex> lock(mu_);
         shadow_valid_ = false;
+        std::vector<std::shared_ptr<HipStorage>> waiting;
+        for (const auto& w : readers_) {
+            auto r = w.lock();
+            if (r && r->deferred_ && r->deferred_->reads(this)) waiting.push_back(std::move(r));
+        }
+        readers_.clear();
+        if (waiting.empty()) return shared_from_this();
+        void* fresh_buffer = nullptr;
+        check(vc_hip_alloc(bytes(), &fresh_buffer), "HIP allocation failed");
+        auto previous = std::make_shared<HipStorage>(elements_, ptr_);
+        ptr_ = fresh_buffer;
+        for (const auto& r : waiting) {
+            r->deferred_->replace(this, previous);
+            previous->readers_.push_back(r);
+        }
+        return previous;
     }
 
 private:
     std::size_t bytes() const { return (elements_ ? elements_ : 1) * sizeof(float); }
 
     std::size_t elements_;
-    mutable std::mutex mu_;
     mutable void* ptr_ = nullptr;
     std::vector<float> shadow_;
-    bool shadow_valid_ = true;
+    mutable std::unique_ptr<DeferredProduct> deferred_;
+    std::vector<std::weak_ptr<HipStorage>> readers_;
+    bool shadow_valid_;
 };
 
 constexpr std::size_t kHostKeptElements = 16;
@@ -307,32 +392,104 @@ std::shared_ptr<Storage> HipBackend::scatter_axis(const Storage& values, std::si
 
 void HipBackend::axpy_inplace(Storage& target, std::size_t target_offset, const Storage& source,
                               std::size_t source_offset, std::size_t count, float alpha) {
-    require(*this);
-    if (target_offset + count > target.size() || source_offset + count > source.size())
-        throw std::out_of_range("HIP axpy exceeds storage");
-    auto& t = as_hip(target);
-    t.written_on_device();
-    if (count == 0) return;
-    check(vc_hip_axpy(t.ptr() + target_offset, dptr(source, source_offset), count, alpha), "HIP axpy failed");
+    axpy_batch({AxpyItem{&target, target_offset, &source, source_offset, count}}, alpha);
 }
 
 void HipBackend::axpy_batch(const std::vector<AxpyItem>& items, float alpha) {
     require(*this);
-    std::vector<float*> targets;
-    std::vector<const float*> sources;
-    std::vector<std::size_t> counts;
     for (const AxpyItem& it : items) {
         if (it.target_offset + it.count > it.target->size() || it.source_offset + it.count > it.source->size())
             throw std::out_of_range("HIP axpy exceeds storage");
+        (void)as_hip(*it.target);
+    }
+    std::vector<std::shared_ptr<const HipStorage>> current;  // kept alive until the launch is enqueued
+    std::vector<float*> outputs;
+    std::vector<const float*> targets, sources;
+    std::vector<std::size_t> counts;
+    for (const AxpyItem& it : items) {
         auto& t = as_hip(*it.target);
-        t.written_on_device();
+        current.push_back(t.before_write());
         if (it.count == 0) continue;
-        targets.push_back(t.ptr() + it.target_offset);
+        outputs.push_back(t.ptr() + it.target_offset);
+        targets.push_back(current.back()->ptr() + it.target_offset);
         sources.push_back(dptr(*it.source, it.source_offset));
         counts.push_back(it.count);
     }
-    if (targets.empty()) return;
-    check(vc_hip_axpy_batch(targets.data(), sources.data(), counts.data(), targets.size(), alpha), "HIP axpy failed");
+    if (outputs.empty()) return;
+    check(vc_hip_axpy_batch(outputs.data(), targets.data(), sources.data(), counts.data(), outputs.size(), alpha),
+          "HIP axpy failed");
+}
+
+namespace {
+std::atomic<bool>& defer_flag() {
+    static std::atomic<bool> flag{[] {
+        const char* v = std::getenv("VECTORCORE_HIP_DEFER");
+        return !(v && std::string(v) == "0");
+    }()};
+    return flag;
+}
+}  // namespace
+
+void HipBackend::set_defer_products(bool enable) { defer_flag() = enable; }
+bool HipBackend::defer_products() const { return defer_flag(); }
+
+std::shared_ptr<Storage> HipBackend::matmul_deferred(const std::shared_ptr<Storage>& a, std::size_t a_offset,
+                                                     const std::shared_ptr<Storage>& b, std::size_t b_offset,
+                                                     std::size_t m, std::size_t k, std::size_t n) {
+    require(*this);
+    if (!defer_products() || m == 0 || k == 0 || n == 0) return nullptr;
+    auto ha = std::dynamic_pointer_cast<HipStorage>(a), hb = std::dynamic_pointer_cast<HipStorage>(b);
+    if (!ha || !hb) throw std::invalid_argument("expected HIP storage");
+    if (a_offset + m * k > ha->size() || b_offset + k * n > hb->size())
+        throw std::out_of_range("HIP matmul operand exceeds storage");
+    DeferredProduct d;
+    d.a = ha;
+    d.b = hb;
+    d.a_offset = a_offset;
+    d.b_offset = b_offset;
+    d.m = m;
+    d.k = k;
+    d.n = n;
+    auto out = std::make_shared<HipStorage>(m * n, std::move(d));
+    ha->add_reader(out);
+    hb->add_reader(out);
+    return out;
+}
+
+std::shared_ptr<Storage> HipBackend::add_bias_deferred(const Storage& product, std::size_t product_offset,
+                                                       const Shape& product_shape, const Strides& product_strides,
+                                                       const std::shared_ptr<Storage>& bias, std::size_t bias_offset,
+                                                       const Shape& bias_shape, const Strides& bias_strides) {
+    const auto* hp = dynamic_cast<const HipStorage*>(&product);
+    auto hbias = std::dynamic_pointer_cast<HipStorage>(bias);
+    if (!hp || !hbias || product_offset != 0 || product_shape.size() != 2) return nullptr;
+    std::optional<DeferredProduct> d = hp->pending();
+    if (!d || d->bias || d->relu || product_shape[0] != d->m || product_shape[1] != d->n ||
+        product_strides != contiguous_strides(product_shape))
+        return nullptr;
+    const bool row = (bias_shape == Shape{d->n} || bias_shape == Shape{1, d->n}) &&
+                     bias_strides == contiguous_strides(bias_shape) && bias_offset + d->n <= hbias->size();
+    if (!row) return nullptr;
+    d->bias = hbias;
+    d->bias_offset = bias_offset;
+    auto out = std::make_shared<HipStorage>(d->m * d->n, *d);
+    d->a->add_reader(out);
+    d->b->add_reader(out);
+    hbias->add_reader(out);
+    return out;
+}
+
+std::shared_ptr<Storage> HipBackend::relu_deferred(const Storage& input, std::size_t offset, std::size_t count) {
+    const auto* h = dynamic_cast<const HipStorage*>(&input);
+    if (!h || offset != 0) return nullptr;
+    std::optional<DeferredProduct> d = h->pending();
+    if (!d || d->relu || count != d->m * d->n) return nullptr;
+    d->relu = true;
+    auto out = std::make_shared<HipStorage>(count, *d);
+    d->a->add_reader(out);
+    d->b->add_reader(out);
+    if (d->bias) d->bias->add_reader(out);
+    return out;
 }
 
 void HipBackend::synchronize() {

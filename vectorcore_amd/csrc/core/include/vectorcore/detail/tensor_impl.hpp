@@ -6,6 +6,7 @@
 
 #include <functional>
 #include <memory>
+#include <optional>
 #include <vector>
 
 namespace vectorcore::detail {
@@ -16,19 +17,20 @@ struct TensorImpl;
 struct GradFn {
     std::vector<std::shared_ptr<TensorImpl>> parents;
     std::function<std::vector<Tensor>(const Tensor&)> backward;
-    // Set by relu(): its saved input (unpacking checks the version). Lets the
-    // engine offer the ReLU mask to the node that produces this node's
-    // upstream gradient (see ReluMaskOffer).
-    std::function<Tensor()> relu_input;
+    // Set by relu(): a tensor whose positive entries are those of the ReLU's
+    // input (the input's version is checked). Lets the engine offer the ReLU
+    // mask to the node that produces this node's upstream gradient (see
+    // ReluMaskOffer).
+    std::function<Tensor()> relu_mask;
 };
 
 // The engine's offer to the backward rule it is about to run: parent 0 of
 // that node is a ReLU output with no other consumer in the graph and no
 // retained gradient, so the rule may return parent 0's gradient already
-// multiplied by [relu input > 0] (the ReLU rule's own arithmetic) and set
+// multiplied by [relu_mask() > 0] (the ReLU rule's own arithmetic) and set
 // `taken`; the engine then passes that gradient through the ReLU node as is.
 struct ReluMaskOffer {
-    std::function<Tensor()> relu_input;
+    std::function<Tensor()> relu_mask;
     bool taken = false;
 };
 // The offer in effect on this thread, or null.
@@ -54,6 +56,8 @@ class SavedTensor {
 public:
     explicit SavedTensor(const Tensor& value);
     [[nodiscard]] Tensor unpack() const;
+    // The tensor if its storage is unchanged since it was saved, else nothing.
+    [[nodiscard]] std::optional<Tensor> unpack_if_unchanged() const;
 private:
     Tensor tensor_;
     std::uint64_t version_;

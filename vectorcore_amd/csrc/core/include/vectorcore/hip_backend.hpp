@@ -76,6 +76,33 @@ public:
     void axpy_batch(const std::vector<AxpyItem>& items, float alpha);
     void synchronize();
 
+    // --- deferred forward products ---
+    // A 2-D product A [m, k] @ B [k, n] (contiguous) can be recorded instead of
+    // launched; it is computed the first time its storage is read. Until then
+    // a row-bias add and a ReLU applied to it become a new deferred product
+    // with that epilogue, computed by one kernel (vc_hip_matmul_bias_relu),
+    // and the partial results nobody reads are never computed. An in-place
+    // write to an operand of a product still deferred first moves the
+    // operand's current buffer to that product (axpy_batch), so results are
+    // those of eager execution. Each returns null when it does not apply; the
+    // caller then runs the op eagerly.
+    [[nodiscard]] std::shared_ptr<Storage> matmul_deferred(const std::shared_ptr<Storage>& a, std::size_t a_offset,
+                                                           const std::shared_ptr<Storage>& b, std::size_t b_offset,
+                                                           std::size_t m, std::size_t k, std::size_t n);
+    // product + bias, product a whole deferred product [m, n] without epilogue
+    // and bias a contiguous [n] or [1, n].
+    [[nodiscard]] std::shared_ptr<Storage> add_bias_deferred(const Storage& product, std::size_t product_offset,
+                                                             const Shape& product_shape, const Strides& product_strides,
+                                                             const std::shared_ptr<Storage>& bias,
+                                                             std::size_t bias_offset, const Shape& bias_shape,
+                                                             const Strides& bias_strides);
+    // relu(input), input a whole deferred product without ReLU.
+    [[nodiscard]] std::shared_ptr<Storage> relu_deferred(const Storage& input, std::size_t offset, std::size_t count);
+    // On by default; VECTORCORE_HIP_DEFER=0 or set_defer_products(false) makes
+    // every product eager.
+    void set_defer_products(bool enable);
+    [[nodiscard]] bool defer_products() const;
+
     // --- fused kernels used by the hip arm of the backward rules ---
     [[nodiscard]] std::shared_ptr<Storage> fill(std::size_t count, float value);
     // out = a op s (scalar_first false) or s op a; s is a host value.

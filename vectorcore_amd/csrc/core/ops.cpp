@@ -220,8 +220,27 @@ std::int64_t uniform_batch_stride(const Shape& batch_axes, const Shape& out_batc
 
 // --- elementwise -------------------------------------------------------------
 
+namespace {
+
+// hip: a row-bias add applied to a product not computed yet joins the
+// product's epilogue (either operand order: fp32 a + b == b + a).
+std::optional<Tensor> add_bias_deferred(const Tensor& a, const Tensor& b) {
+    if (a.device() != Device::hip() || b.device() != Device::hip()) return std::nullopt;
+    for (int order = 0; order < 2; ++order) {
+        const Tensor& product = order == 0 ? a : b;
+        const Tensor& bias = order == 0 ? b : a;
+        auto s = hip().add_bias_deferred(st(product), off(product), product.shape(), product.strides(),
+                                         bias.impl()->storage, off(bias), bias.shape(), bias.strides());
+        if (s) return detail::make_tensor(std::move(s), product.shape(), false);
+    }
+    return std::nullopt;
+}
+
+}  // namespace
+
 Tensor add(const Tensor& a, const Tensor& b) {
-    auto out = binary_forward(a, b, cpu::BinaryOp::Add);
+    std::optional<Tensor> fused = add_bias_deferred(a, b);
+    auto out = fused ? *fused : binary_forward(a, b, cpu::BinaryOp::Add);
     const Shape as = a.shape(), bs = b.shape();
     const bool na = a.requires_grad(), nb = b.requires_grad();
     detail::attach_grad_fn(out, {a, b}, [=](const Tensor& g) {
@@ -284,8 +303,26 @@ Tensor negate(const Tensor& v) {
 
 // --- matrix products -------------------------------------------------------------
 
+namespace {
+
+// hip: a 2-D product is recorded and computed on first use, so that a
+// following bias add and ReLU can join its epilogue (HipBackend::matmul_deferred).
+std::optional<Tensor> matmul_deferred(const Tensor& a, const Tensor& b) {
+    if (a.device() != Device::hip() || b.device() != Device::hip() || a.ndim() != 2 || b.ndim() != 2)
+        return std::nullopt;
+    if (a.strides() != contiguous_strides(a.shape()) || b.strides() != contiguous_strides(b.shape()))
+        return std::nullopt;
+    const MatmulPlan p = plan_matmul(a, b, false, false);
+    auto s = hip().matmul_deferred(a.impl()->storage, off(a), b.impl()->storage, off(b), p.m, p.k, p.n);
+    if (!s) return std::nullopt;
+    return detail::make_tensor(std::move(s), Shape{p.m, p.n}, false);
+}
+
+}  // namespace
+
 Tensor matmul(const Tensor& a, const Tensor& b) {
-    auto out = matmul_kernel(a, b, false, false);
+    std::optional<Tensor> deferred = matmul_deferred(a, b);
+    auto out = deferred ? *deferred : matmul_kernel(a, b, false, false);
     const detail::SavedTensor sa(a), sb(b);
     const Shape as = a.shape(), bs = b.shape();
     const bool na = a.requires_grad(), nb = b.requires_grad();
@@ -310,15 +347,15 @@ Tensor matmul(const Tensor& a, const Tensor& b) {
                 Shape product = p.out_batch;
                 product.push_back(p.m);
                 product.push_back(p.k);
-                std::optional<Tensor> relu_input;
+                std::optional<Tensor> relu_mask;
                 if (offer && product == as) {
-                    relu_input = offer->relu_input();
-                    if (relu_input->device() != Device::hip() || relu_input->shape() != as ||
-                        relu_input->strides() != contiguous_strides(as))
-                        relu_input.reset();
+                    relu_mask = offer->relu_mask();
+                    if (relu_mask->device() != Device::hip() || relu_mask->shape() != as ||
+                        relu_mask->strides() != contiguous_strides(as))
+                        relu_mask.reset();
                 }
-                if (relu_input) {
-                    grads[0] = matmul_kernel(g, bv, false, true, &*relu_input);
+                if (relu_mask) {
+                    grads[0] = matmul_kernel(g, bv, false, true, &*relu_mask);
                     offer->taken = true;
                 } else {
                     grads[0] = detail::sum_to_shape(matmul_kernel(g, bv, false, true), as);
@@ -460,12 +497,23 @@ Tensor log(const Tensor& v) {
 }
 
 Tensor relu(const Tensor& v) {
-    auto out = unary_forward(v, cpu::UnaryOp::Relu);
-    const detail::SavedTensor saved(v);
-    detail::attach_grad_fn(out, {v}, [saved](const Tensor& g) {
-        return std::vector<Tensor>{activation_grad(HipBackend::Activation::Relu, g, saved.unpack())};
+    std::shared_ptr<Storage> fused;
+    if (v.device() == Device::hip()) fused = hip().relu_deferred(st(v), off(v), v.numel());
+    auto out = fused ? detail::make_tensor(std::move(fused), v.shape(), false) : unary_forward(v, cpu::UnaryOp::Relu);
+    // The rule's mask [input > 0] is also [output > 0]: relu keeps exactly the
+    // positive entries. It is read from the output while that is unchanged,
+    // so an input that is a deferred product never has to be computed; the
+    // input's version is checked either way, as the reference's rule does.
+    const detail::SavedTensor saved(v), saved_out(out);
+    const auto mask = [saved, saved_out] {
+        const Tensor input = saved.unpack();
+        std::optional<Tensor> output = saved_out.unpack_if_unchanged();
+        return output ? *output : input;
+    };
+    detail::attach_grad_fn(out, {v}, [mask](const Tensor& g) {
+        return std::vector<Tensor>{activation_grad(HipBackend::Activation::Relu, g, mask())};
     });
-    if (out.impl()->grad_fn) out.impl()->grad_fn->relu_input = [saved] { return saved.unpack(); };
+    if (out.impl()->grad_fn) out.impl()->grad_fn->relu_mask = mask;
     return out;
 }
 

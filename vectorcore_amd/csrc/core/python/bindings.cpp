@@ -213,6 +213,17 @@ PYBIND11_MODULE(_vectorcore, m) {
             check(vc_hip_profile_enable(enable ? 1 : 0));
         },
         py::arg("enable"), py::arg("labels") = py::none());
+    m.def(
+        "hip_defer_products",
+        [](std::optional<bool> enable) {
+            auto& b = HipBackend::instance();
+            const bool previous = b.defer_products();
+            if (enable) b.set_defer_products(*enable);
+            return previous;
+        },
+        py::arg("enable") = py::none(),
+        "Whether 2-D hip products are computed on first use (fusing a following bias add and ReLU); "
+        "sets it when `enable` is given and returns the previous setting.");
     m.def("hip_profile_reset", [] { check(vc_hip_profile_reset()); });
     m.def("hip_profile_read", [] {
         std::size_t n = 0;

@@ -312,10 +312,10 @@ void Tensor::backward(const Tensor& gradient) const {
             const auto& first = node->grad_fn->parents.empty() ? nullptr : node->grad_fn->parents[0];
             detail::ReluMaskOffer offer;
             const bool offered = first && upstream.device() == Device::hip() && first->grad_fn &&
-                                 first->grad_fn->relu_input && first->requires_grad && !first->leaf &&
+                                 first->grad_fn->relu_mask && first->requires_grad && !first->leaf &&
                                  !first->retains_grad && consumers[first.get()] == 1;
             if (offered) {
-                offer.relu_input = first->grad_fn->relu_input;
+                offer.relu_mask = first->grad_fn->relu_mask;
                 detail::set_relu_mask_offer(&offer);
             }
             try {

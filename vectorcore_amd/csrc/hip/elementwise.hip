@@ -119,13 +119,15 @@ __global__ __launch_bounds__(kBlock) void map2_kernel(const float* __restrict__ 
     if (t < tail) y[4 * n4 + t] = f(a[4 * n4 + t], b[4 * n4 + t]);
 }
 
-// SGD over a list of parameters in one launch: t_k += alpha * s_k for every
-// tensor k, as the per-tensor axpy computes it. The tensors are laid end to
-// end in 16-byte chunks (first[k] = chunks before tensor k); a thread finds its
-// tensor by a short scan. Each tensor's last chunk may be partial.
+// SGD over a list of parameters in one launch: o_k = t_k + alpha * s_k for
+// every tensor k (o_k == t_k in place), as the per-tensor axpy computes it.
+// The tensors are laid end to end in 16-byte chunks (first[k] = chunks before
+// tensor k); a thread finds its tensor by a short scan. Each tensor's last
+// chunk may be partial.
 constexpr int kAxpyList = 16;
 struct AxpyList {
-    float* t[kAxpyList];
+    float* o[kAxpyList];
+    const float* t[kAxpyList];
     const float* s[kAxpyList];
     int64_t count[kAxpyList];
     int64_t first[kAxpyList + 1];
@@ -141,12 +143,13 @@ __global__ __launch_bounds__(kBlock) void axpy_list_kernel(AxpyList L) {
         int k = 0;
         while (c >= L.first[k + 1]) ++k;
         const int64_t e = (c - L.first[k]) * 4;
-        float* t = L.t[k] + e;
+        float* o = L.o[k] + e;
+        const float* t = L.t[k] + e;
         const float* src = L.s[k] + e;
         if (e + 4 <= L.count[k]) {
-            st4(t, apply4(f, ld4(t), ld4(src)));
+            st4(o, apply4(f, ld4(t), ld4(src)));
         } else {
-            for (int64_t i = 0; e + i < L.count[k]; ++i) t[i] = f(t[i], src[i]);
+            for (int64_t i = 0; e + i < L.count[k]; ++i) o[i] = f(t[i], src[i]);
         }
     }
 }
@@ -405,11 +408,12 @@ int vc_hip_axpy(float* target, const float* source, size_t count, float alpha) {
     return guard([&] { launch_map2("axpy", target, source, target, count, AxpyOp{alpha}, 12.0); });
 }
 
-int vc_hip_axpy_batch(float* const* targets, const float* const* sources, const size_t* counts, size_t tensors,
-                      float alpha) {
+int vc_hip_axpy_batch(float* const* outputs, const float* const* targets, const float* const* sources,
+                      const size_t* counts, size_t tensors, float alpha) {
     return guard([&] {
         Device& d = require_device();
-        if (tensors > 0 && (!targets || !sources || !counts)) fail(VC_HIP_ERR_INVALID_ARGUMENT, "axpy_batch: null list");
+        if (tensors > 0 && (!outputs || !targets || !sources || !counts))
+            fail(VC_HIP_ERR_INVALID_ARGUMENT, "axpy_batch: null list");
         size_t i = 0;
         while (i < tensors) {
             AxpyList L{};
@@ -418,11 +422,12 @@ int vc_hip_axpy_batch(float* const* targets, const float* const* sources, const 
             // tensor goes through the single-tensor kernel on its own.
             for (; i < tensors && L.n < kAxpyList; ++i) {
                 if (counts[i] == 0) continue;
-                if (!targets[i] || !sources[i]) fail(VC_HIP_ERR_INVALID_ARGUMENT, "axpy_batch: null buffer");
-                if (!aligned16(targets[i]) || !aligned16(sources[i])) {
-                    launch_map2("axpy", targets[i], sources[i], targets[i], counts[i], AxpyOp{alpha}, 12.0);
+                if (!outputs[i] || !targets[i] || !sources[i]) fail(VC_HIP_ERR_INVALID_ARGUMENT, "axpy_batch: null buffer");
+                if (!aligned16(outputs[i]) || !aligned16(targets[i]) || !aligned16(sources[i])) {
+                    launch_map2("axpy", targets[i], sources[i], outputs[i], counts[i], AxpyOp{alpha}, 12.0);
                     continue;
                 }
+                L.o[L.n] = outputs[i];
                 L.t[L.n] = targets[i];
                 L.s[L.n] = sources[i];
                 L.count[L.n] = int64_t(counts[i]);

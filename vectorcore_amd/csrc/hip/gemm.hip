@@ -63,7 +63,16 @@ struct GemmArgs {
     int kt_per_split;              //   reduce == 1: BK slices of K per split
     int64_t r_per_split;           //   reduce > 1: products r per split
     const float* relu_mask;        // null, or [batch][M][N]: C *= [relu_mask > 0] (fused ReLU backward)
+    const float* bias;             // null, or [N]: C += bias[column] (fused row-bias add)
+    int relu;                      // nonzero: C = C > 0 ? C : 0 after the bias (fused ReLU forward)
 };
+
+// The forward epilogue, in the order of the unfused ops: the row-broadcast add
+// (a + b in fp32), then relu (x > 0 ? x : 0).
+__device__ inline float bias_relu(float value, float bias, bool relu) {
+    value = value + bias;
+    return relu ? (value > 0.0f ? value : 0.0f) : value;
+}
 
 // Tile id -> (tile_m, tile_n) with the XCD remap and grouped order.
 __device__ inline void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -366,6 +375,28 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
                         acc[i][j][v] = value * (xv > 0.0f ? 1.0f : 0.0f);
                     }
         }
+        if (p.splits == 1 && (p.bias || p.relu)) {  // forward epilogue: + bias[column], then ReLU
+            float bias[2] = {0.0f, 0.0f};
+            if (p.bias) {
+                const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.bias + n0);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int col = wn + 32 * j + (lane & 31);
+                    bias[j] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rb, col < col_lim ? uint32_t(col) * 4u : kOutOfRange,
+                                                                    0, 0));
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const float value = acc[i][j][v];
+                        acc[i][j][v] = bias_relu(value, bias[j], p.relu != 0);
+                    }
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -385,10 +416,11 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
 }
 
 // Split combine: c[z][i] = sum over s of part[z][s][i], in split order, then
-// the fused ReLU mask when there is one.
+// the fused ReLU mask or the forward epilogue when there is one.
 __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ part, float* __restrict__ c,
-                                                        int64_t batch, int64_t mn, int splits,
-                                                        const float* __restrict__ relu_mask) {
+                                                        int64_t batch, int64_t mn, int64_t n, int splits,
+                                                        const float* __restrict__ relu_mask,
+                                                        const float* __restrict__ bias, int relu) {
     const int64_t total = batch * mn;
     const int64_t stride = int64_t(gridDim.x) * blockDim.x;
     for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
@@ -397,6 +429,7 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
         float acc = src[0];
         for (int s = 1; s < splits; ++s) acc += src[int64_t(s) * mn];
         if (relu_mask) acc = acc * (relu_mask[t] > 0.0f ? 1.0f : 0.0f);
+        if (bias || relu) acc = bias_relu(acc, bias ? bias[i % n] : 0.0f, relu != 0);
         c[t] = acc;
     }
 }
@@ -430,6 +463,7 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
         if (row < p.M && col < p.N) {
             const int64_t t = z * p.M * p.N + row * p.N + col;
             if (p.relu_mask) acc = acc * (p.relu_mask[t] > 0.0f ? 1.0f : 0.0f);
+            if (p.bias || p.relu) acc = bias_relu(acc, p.bias ? p.bias[col] : 0.0f, p.relu != 0);
             p.c[t] = acc;
         }
     }
@@ -453,7 +487,7 @@ const char* variant_label(bool ta, bool tb) {
 // offsets: nullptr for the affine mode (a_bstride / b_bstride).
 void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t a_bstride,
           int64_t b_bstride, const std::vector<int64_t>* offsets, int64_t reduce, int64_t a_rstride, int64_t b_rstride,
-          bool ta, bool tb, const float* relu_mask = nullptr) {
+          bool ta, bool tb, const float* relu_mask = nullptr, const float* bias = nullptr, bool relu = false) {
     Device& d = require_device();
     if (M < 0 || N < 0 || K < 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "negative matrix dimension");
     if (M == 0 || N == 0 || batch == 0) return;
@@ -528,8 +562,11 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     const char* label = variant_label(ta, tb);
     const double flops = 2.0 * double(M) * double(N) * double(K) * double(batch) * double(reduce);
     args.relu_mask = relu_mask;
+    args.bias = bias;
+    args.relu = relu ? 1 : 0;
     const double bytes =
-        4.0 * (double(M * K + K * N) * double(reduce) + double(M * N) * (relu_mask ? 2.0 : 1.0)) * double(batch);
+        4.0 * (double(M * K + K * N) * double(reduce) + double(M * N) * (relu_mask ? 2.0 : 1.0)) * double(batch) +
+        (bias ? 4.0 * double(N) : 0.0);
     Profiled prof(label, flops, bytes);
     if (ta && tb) launch_variant<true, true>(args, vec, simple, grid, d.stream);
     else if (ta) launch_variant<true, false>(args, vec, simple, grid, d.stream);
@@ -539,7 +576,8 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
         after_launch(label);
         const int64_t total = batch * M * N;
         launch(split_sum_kernel, dim3(unsigned(std::min<int64_t>((total + 255) / 256, int64_t(d.cu_count) * 16))),
-                           dim3(256), 0, d.stream, partials.as<float>(), c, batch, M * N, splits, relu_mask);
+                           dim3(256), 0, d.stream, partials.as<float>(), c, batch, M * N, N, splits, relu_mask, bias,
+                           args.relu);
     }
     after_launch(label);
     prof.done();
@@ -588,6 +626,16 @@ int vc_hip_matmul_relu_mask(const float* a, const float* b, float* c, size_t m, 
     return guard([&] {
         if (!relu_input) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask: null ReLU input");
         matmul_offsets(a, b, c, m, k, n, a_offsets, b_offsets, batch, trans_a, trans_b, relu_input);
+    });
+}
+
+int vc_hip_matmul_bias_relu(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                            const float* bias, int relu) {
+    return guard([&] {
+        if (m == 0 || n == 0) return;
+        if (k == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_bias_relu needs k > 0");
+        gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), 1, 0, 0, nullptr, 1, 0, 0, false, false, nullptr, bias,
+             relu != 0);
     });
 }
 

@@ -343,14 +343,16 @@ def test_scatter_and_transpose_exact():
         np.testing.assert_array_equal(dout.numpy(), K.transpose_last2(t))
 
 
-def xent_dev(logits, targets):
+def xent_dev(logits, targets, with_stats=False):
     rows, classes = logits.shape
-    dl, dt = C.Buffer.of(logits), C.Buffer.of(targets.astype(np.int32), dtype=np.int32)
+    dl, dt = C.Buffer.of(logits), C.Buffer.of(np.asarray(targets).astype(np.int32), dtype=np.int32)
     stats, loss = C.Buffer((rows, 2)), C.Buffer((1,))
     C.check(C.lib().vc_hip_xent_forward(dl.ptr, dt.ptr, rows, classes, stats.ptr, loss.ptr))
     one = C.Buffer.of(np.ones(1, dtype=np.float32))
     grad = C.Buffer(logits.shape)
     C.check(C.lib().vc_hip_xent_backward(dl.ptr, dt.ptr, stats.ptr, one.ptr, rows, classes, grad.ptr))
+    if with_stats:
+        return loss.numpy()[0], grad.numpy(), stats.numpy()
     return loss.numpy()[0], grad.numpy()
 
 
@@ -370,6 +372,60 @@ def test_cross_entropy_against_oracle(rows, classes):
     ref_loss.backward()
     np.testing.assert_allclose(loss, ref_loss.data, rtol=1e-6)
     np.testing.assert_allclose(grad, t.grad.data, rtol=1e-5, atol=1e-9)
+
+
+def _special_rows(classes, rng):
+    """Rows that exercise the max and non-finite rules, with their targets."""
+    base = lambda: -np.abs(rng.standard_normal(classes)).astype(np.float32) - 0.5
+    rows, targets = [], []
+
+    def add(row, t):
+        rows.append(row)
+        targets.append(t)
+
+    r = base(); r[3], r[classes - 2] = -0.0, 0.0; add(r, 1)      # zero maximum, -0.0 first
+    r = base(); r[2], r[classes - 1] = 0.0, -0.0; add(r, 0)      # zero maximum, +0.0 first
+    add(np.full(classes, -np.inf, np.float32), 1)                # all -inf: m = -inf
+    r = base(); r[0] = np.nan; add(r, 1)                         # NaN element 0 is the max
+    r = base(); r[classes // 2] = np.nan; add(r, 0)              # NaN elsewhere: skipped by max, NaN term
+    r = base(); r[1] = np.inf; add(r, 0)                         # +inf maximum
+    r = base(); r[classes - 1] = -np.inf; add(r, 0)              # -inf off the target: NaN term
+    r = base(); r[2] = -np.inf; add(r, 2)                        # -inf at the target: term -inf
+    r = base(); r[classes - 3] = 30.0; add(r, classes - 3)       # ordinary, target is the maximum
+    return np.stack(rows), targets
+
+
+@pytest.mark.parametrize("classes", [1000, 40, 37, 4100])
+def test_cross_entropy_special_values_match_the_oracle(classes):
+    # 1000 and 40 take the register-held row kernel, 37 (not a multiple of 4)
+    # and 4100 (too long for registers) the streaming one. Each row alone, so
+    # one NaN row does not hide the others; the row maximum must carry the
+    # reference's sign of zero.
+    from oracle import autograd as A
+    rows, targets = _special_rows(classes, np.random.default_rng(classes))
+    for i, (row, t) in enumerate(zip(rows, targets)):
+        logits = row[None, :]
+        loss, grad, stats = xent_dev(logits, [t], with_stats=True)
+        ref = A.T(logits, True)
+        ref_loss = A.cross_entropy(ref, [t])
+        ref_loss.backward()
+        np.testing.assert_allclose(loss, ref_loss.data, rtol=1e-6, equal_nan=True, err_msg=f"row {i}")
+        np.testing.assert_allclose(grad, ref.grad.data, rtol=1e-5, atol=1e-9, equal_nan=True, err_msg=f"row {i}")
+        m = K.reduce_axis(logits, 1, K.MAX)[0]
+        if np.isnan(m):
+            assert np.isnan(stats[0, 0]), f"row {i}"
+        else:
+            assert stats[0, 0].view(np.uint32) == np.float32(m).view(np.uint32), f"row {i}: {stats[0, 0]} vs {m}"
+    # the finite rows together, many times over: the per-block loss partials
+    keep = [0, 1, 8]
+    many = np.concatenate([rows[keep]] * 700)
+    many_t = [targets[k] for k in keep] * 700
+    loss, grad = xent_dev(many, many_t)
+    ref = A.T(many, True)
+    ref_loss = A.cross_entropy(ref, many_t)
+    ref_loss.backward()
+    np.testing.assert_allclose(loss, ref_loss.data, rtol=1e-6)
+    np.testing.assert_allclose(grad, ref.grad.data, rtol=1e-5, atol=1e-9)
 
 
 def test_pool_reuses_released_buffers():

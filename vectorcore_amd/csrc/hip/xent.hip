@@ -53,60 +53,101 @@ __device__ inline float row_max(const float* row, int64_t len, int lane, bool ve
 }
 
 // Lane 0: the row's statistics (max, exp-sum) and its loss term
-// shifted_t - log(s), NaN when a non-target log-prob is not finite.
-__device__ inline void write_row(const float* __restrict__ row, int64_t r, int64_t len, int t, float m, double acc,
-                                 int bad, float* __restrict__ stats, float* __restrict__ terms) {
+// shifted_t - log(s) (x_t the target's logit), NaN when a non-target log-prob
+// is not finite or the target is outside the row (never with checked
+// targets). Returns the term.
+__device__ inline float write_row(int64_t r, int64_t len, int t, float x_t, float m, double acc, int bad,
+                                  float* __restrict__ stats) {
     const float s = float(acc);
     const float L = logf(s);
     float term;
     if (t < 0 || int64_t(t) >= len) {
-        term = __builtin_nanf("");  // never reached with checked targets; no out-of-row read
+        term = __builtin_nanf("");
     } else {
-        const float shifted = row[t] - m;
+        const float shifted = x_t - m;
         term = bad ? __builtin_nanf("") : shifted - L;
     }
     stats[2 * r] = m;
     stats[2 * r + 1] = s;
-    terms[r] = term;
+    return term;
+}
+
+// Largest value over the wavefront (inputs never NaN). Lanes can disagree
+// only on the sign of a zero maximum, which the caller decides exactly.
+__device__ inline float wave_max(float v) {
+    const int lane = red::lane_id();
+    float o = red::partner<0>(v, lane);
+    v = o > v ? o : v;
+    o = red::partner<1>(v, lane);
+    v = o > v ? o : v;
+    o = red::partner<2>(v, lane);
+    v = o > v ? o : v;
+    o = red::partner<3>(v, lane);
+    v = o > v ? o : v;
+    o = red::partner<4>(v, lane);
+    v = o > v ? o : v;
+    o = red::partner<5>(v, lane);
+    return o > v ? o : v;
 }
 
 // Row statistics and loss term of one row from values in registers (NV
 // float4 per lane; element a = 4 lane + 256 u + component, a multiple-of-4
-// row of at most 256 NV classes). Each lane visits its elements in ascending
-// order, as the streaming path does, so both give the same bits.
+// row of at most 256 NV classes; elements past the row hold -inf). Each lane
+// visits its elements in ascending order, as the streaming path does, so both
+// give the same bits. Returns the loss term on lane 0.
 template <int NV>
-__device__ inline void finish_row(const f4 (&v)[NV], const float* __restrict__ row, int64_t r, int64_t len, int t,
-                                  int lane, float* __restrict__ stats, float* __restrict__ terms) {
-    Best b = red::no_best();
+__device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, int t, int lane,
+                                   float* __restrict__ stats) {
+    // The reference's max is the first strict maximum, skipping NaN after
+    // element 0. Its value is the largest non-NaN element, whichever index
+    // holds it, except for the sign of a zero maximum (the first zero wins)
+    // and a NaN element 0, both settled below.
+    float mx = -__builtin_inff();
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
-        const int a = lane * 4 + u * kWave * 4;
-        if (a < len) {
-            red::consider_ordered(b, v[u].x, a);
-            red::consider_ordered(b, v[u].y, a + 1);
-            red::consider_ordered(b, v[u].z, a + 2);
-            red::consider_ordered(b, v[u].w, a + 3);
-        }
+        mx = v[u].x > mx ? v[u].x : mx;
+        mx = v[u].y > mx ? v[u].y : mx;
+        mx = v[u].z > mx ? v[u].z : mx;
+        mx = v[u].w > mx ? v[u].w : mx;
     }
-    b = red::wave_best(b);
+    mx = wave_max(mx);
     const float first = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v[0].x)));
-    const float m = first != first ? first : b.v;  // max() keeps a NaN first element (src/cpu/cpu_backend.cpp:443-452)
+    float m;
+    if (first != first) {
+        m = first;  // max() keeps a NaN first element (src/cpu/cpu_backend.cpp:443-452)
+    } else if (mx == 0.0f) {  // rare: which zero comes first
+        Best b = red::no_best();
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const int a = lane * 4 + u * kWave * 4;
+            if (a < len) {
+                red::consider_ordered(b, v[u].x, a);
+                red::consider_ordered(b, v[u].y, a + 1);
+                red::consider_ordered(b, v[u].z, a + 2);
+                red::consider_ordered(b, v[u].w, a + 3);
+            }
+        }
+        m = red::wave_best(b).v;
+    } else {
+        m = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, mx)));
+    }
     // exp via the hardware exp2 (V_EXP_F32, 1 ulp) of s * log2(e): the
     // rounding of the product adds |s| 2^-24 relative error, at most ~2e-7 on
     // the terms within e^-3 of the row maximum, which carry the sum (s <= 0).
+    // Elements past the row give exp(-inf - m) = 0 (or NaN when m is -inf or
+    // NaN, and then every real element's term is NaN too): adding them leaves
+    // the sum unchanged.
     double acc = 0.0;
-    bool nonfinite = false;  // any shifted value not finite, target included
+    bool nonfinite = false;  // any shifted value in the row not finite, target included
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
         const int a = lane * 4 + u * kWave * 4;
-        if (a < len) {
-            const float s0 = v[u].x - m, s1 = v[u].y - m, s2 = v[u].z - m, s3 = v[u].w - m;
-            acc += double(__expf(s0));
-            acc += double(__expf(s1));
-            acc += double(__expf(s2));
-            acc += double(__expf(s3));
-            nonfinite |= !isfinite(s0) | !isfinite(s1) | !isfinite(s2) | !isfinite(s3);
-        }
+        const float s0 = v[u].x - m, s1 = v[u].y - m, s2 = v[u].z - m, s3 = v[u].w - m;
+        acc += double(__expf(s0));
+        acc += double(__expf(s1));
+        acc += double(__expf(s2));
+        acc += double(__expf(s3));
+        nonfinite |= (a < len) & (!isfinite(s0) | !isfinite(s1) | !isfinite(s2) | !isfinite(s3));
     }
     int bad = 0;  // a non-target log-prob that is not finite
     if (__ballot(nonfinite) != 0) {  // rare: decide exactly, leaving the target out
@@ -122,7 +163,19 @@ __device__ inline void finish_row(const f4 (&v)[NV], const float* __restrict__ r
     }
     acc = red::wave_sum(acc);
     bad = red::wave_or(bad);
-    if (lane == 0) write_row(row, r, len, t, m, acc, bad, stats, terms);
+    // The target's logit from the registers of the lane holding it (t is
+    // wave-uniform): element t is component t % 4 of v[t / 256] on lane
+    // (t / 4) % 64.
+    float x_t = 0.0f;
+    if (t >= 0 && int64_t(t) < len) {
+        const int tu = t >> 8, tc = t & 3, owner = (t >> 2) & 63;
+        float mine = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NV; ++u)
+            if (u == tu) mine = tc == 0 ? v[u].x : tc == 1 ? v[u].y : tc == 2 ? v[u].z : v[u].w;
+        x_t = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), owner));
+    }
+    return lane == 0 ? write_row(r, len, t, x_t, m, acc, bad, stats) : 0.0f;
 }
 
 template <int NV>
@@ -130,30 +183,49 @@ __device__ inline void load_row(f4 (&v)[NV], const float* __restrict__ row, int6
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
         const int64_t a = int64_t(lane) * 4 + int64_t(u) * kWave * 4;
-        v[u] = a < len ? ld4(row + a) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+        const float pad = -__builtin_inff();
+        v[u] = a < len ? ld4(row + a) : f4{pad, pad, pad, pad};
     }
 }
 
 // Rows held in registers. Each wavefront walks rows r, r + W, ... (W
-// wavefronts in the grid) and loads its next row before working on the
-// current one, so memory latency overlaps the exp work of the row before.
+// wavefronts in the grid) and loads its next row (and target) before working
+// on the current one, so memory latency overlaps the exp work of the row
+// before. The loss terms are summed on the way: each wavefront in row order,
+// then the block's wavefronts in order, into one double per block.
 template <int NV>
 __global__ __launch_bounds__(kBlock) void xent_rows_cached_kernel(const float* __restrict__ x,
                                                                   const int* __restrict__ targets, int64_t rows,
                                                                   int64_t len, float* __restrict__ stats,
-                                                                  float* __restrict__ terms) {
+                                                                  double* __restrict__ part) {
+    __shared__ double wave_terms[kRowsPerBlock];
     const int lane = threadIdx.x % kWave;
     const int64_t first = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
     const int64_t waves = int64_t(gridDim.x) * kRowsPerBlock;
-    if (first >= rows) return;
-    f4 cur[NV], next[NV];
-    load_row(cur, x + first * len, len, lane);
-    for (int64_t r = first; r < rows; r += waves) {
-        const int64_t rn = r + waves;
-        if (rn < rows) load_row(next, x + rn * len, len, lane);
-        finish_row(cur, x + r * len, r, len, targets[r], lane, stats, terms);
+    double total = 0.0;  // lane 0: this wavefront's terms
+    if (first < rows) {
+        f4 cur[NV], next[NV];
+        load_row(cur, x + first * len, len, lane);
+        int t = __builtin_amdgcn_readfirstlane(targets[first]);
+        for (int64_t r = first; r < rows; r += waves) {
+            const int64_t rn = r + waves;
+            int tn = 0;
+            if (rn < rows) {
+                load_row(next, x + rn * len, len, lane);
+                tn = __builtin_amdgcn_readfirstlane(targets[rn]);
+            }
+            total += double(finish_row(cur, r, len, t, lane, stats));
 #pragma unroll
-        for (int u = 0; u < NV; ++u) cur[u] = next[u];
+            for (int u = 0; u < NV; ++u) cur[u] = next[u];
+            t = tn;
+        }
+    }
+    if (lane == 0) wave_terms[threadIdx.x / kWave] = total;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double sum = wave_terms[0];
+        for (int w = 1; w < kRowsPerBlock; ++w) sum += wave_terms[w];
+        part[blockIdx.x] = sum;
     }
 }
 
@@ -191,7 +263,10 @@ __global__ __launch_bounds__(kBlock) void xent_rows_kernel(const float* __restri
     }
     acc = red::wave_sum(acc);
     bad = red::wave_or(bad);
-    if (lane == 0) write_row(row, r, len, t, m, acc, bad, stats, terms);
+    if (lane == 0) {
+        const bool in_row = t >= 0 && int64_t(t) < len;
+        terms[r] = write_row(r, len, t, in_row ? row[t] : 0.0f, m, acc, bad, stats);
+    }
 }
 
 // loss = -(float)(sum of row terms) / (float)rows: negate, then divide, as
@@ -258,28 +333,34 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         const int64_t nv = vec ? (C + kWave * 4 - 1) / (kWave * 4) : 0;
         const unsigned cached_grid = unsigned(std::min<int64_t>((R + kRowsPerBlock - 1) / kRowsPerBlock,
                                                                 int64_t(d.cu_count) * 8));
-#define VC_XENT_ROWS(NV)                                                                                       \
-    launch((xent_rows_cached_kernel<NV>), dim3(cached_grid), dim3(kBlock), 0, d.stream, logits, targets, R, C, \
-           row_stats, terms.as<float>())
-        if (!vec || nv > 16)
+        int64_t blocks = 0;  // loss partials, one double each
+        Scratch part(size_t(std::max<int64_t>(cached_grid, (R + red::sum_chunk(R) - 1) / red::sum_chunk(R))) *
+                     sizeof(double));
+        if (!vec || nv > 16) {
+            // Row terms, then the shared deterministic two-stage sum.
             launch((vec ? xent_rows_kernel<true> : xent_rows_kernel<false>), dim3(grid), dim3(kBlock), 0, d.stream,
                    logits, targets, R, C, row_stats, terms.as<float>());
-        else if (nv <= 1) VC_XENT_ROWS(1);
-        else if (nv <= 2) VC_XENT_ROWS(2);
-        else if (nv <= 4) VC_XENT_ROWS(4);
-        else if (nv <= 8) VC_XENT_ROWS(8);
-        else VC_XENT_ROWS(16);
+            after_launch("xent_forward");
+            const int64_t chunk = red::sum_chunk(R);
+            blocks = (R + chunk - 1) / chunk;
+            launch(red::sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream,
+                   terms.as<float>(), part.as<double>(), R, chunk);
+        } else {
+            // Register-held rows; the row kernel sums the terms per block.
+#define VC_XENT_ROWS(NV)                                                                                       \
+    launch((xent_rows_cached_kernel<NV>), dim3(cached_grid), dim3(kBlock), 0, d.stream, logits, targets, R, C, \
+           row_stats, part.as<double>())
+            if (nv <= 1) VC_XENT_ROWS(1);
+            else if (nv <= 2) VC_XENT_ROWS(2);
+            else if (nv <= 4) VC_XENT_ROWS(4);
+            else if (nv <= 8) VC_XENT_ROWS(8);
+            else VC_XENT_ROWS(16);
 #undef VC_XENT_ROWS
-        after_launch("xent_forward");
-        // Row terms -> loss with the shared deterministic two-stage sum.
-        const int64_t chunk = red::sum_chunk(R);
-        const int64_t blocks = (R + chunk - 1) / chunk;
-        Scratch part(size_t(blocks) * sizeof(double));
-        launch(red::sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream,
-                           terms.as<float>(), part.as<double>(), R, chunk);
+            blocks = cached_grid;
+        }
         after_launch("xent_forward");
         launch(red::sum_final_kernel<NegateDivide>, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), loss,
-                           blocks, NegateDivide{float(R)});
+               blocks, NegateDivide{float(R)});
         after_launch("xent_forward");
         p.done();
     });

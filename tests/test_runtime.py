@@ -462,6 +462,26 @@ def test_deferred_product_shared_reshaped_and_as_a_bias():
 
 
 @hip_only
+def test_long_chain_of_deferred_products():
+    # 3000 products, each of the one before, none read until the end: the
+    # chain is computed in bounded pieces and gives the eager bits.
+    rng = np.random.default_rng(10)
+    xs = rng.standard_normal((8, 8)).astype(np.float32)
+    ws = (np.eye(8) + 0.01 * rng.standard_normal((8, 8))).astype(np.float32)
+    bs = (0.01 * rng.standard_normal(8)).astype(np.float32)
+
+    def run():
+        x, w, b = (vc.Tensor(v, device="hip") for v in (xs, ws, bs))
+        for _ in range(3000):
+            x = (x @ w + b).relu()
+        return [npy(x)]
+
+    eager, deferred = _eager_then_deferred(run)
+    _assert_same_bits(eager, deferred)
+    assert np.isfinite(deferred[0]).all()
+
+
+@hip_only
 def test_relu_rule_falls_back_to_its_input_when_the_output_changes():
     rng = np.random.default_rng(9)
     xs, ws = rng.standard_normal((6, 5)).astype(np.float32), rng.standard_normal((5, 4)).astype(np.float32)

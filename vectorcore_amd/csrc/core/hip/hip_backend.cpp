@@ -52,6 +52,7 @@ struct DeferredProduct {
     std::size_t a_offset = 0, b_offset = 0, bias_offset = 0;
     std::size_t m = 0, k = 0, n = 0;
     bool relu = false;
+    int depth = 1;  // 1 + the deepest deferred operand: computing it recurses this deep
 
     [[nodiscard]] bool reads(const HipStorage* s) const { return a.get() == s || b.get() == s || bias.get() == s; }
     void replace(const HipStorage* s, const std::shared_ptr<HipStorage>& with) {
@@ -127,6 +128,12 @@ public:
         return *deferred_;
     }
 
+    // How deep computing this storage would recurse (0: nothing deferred).
+    int pending_depth() const {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        return deferred_ ? deferred_->depth : 0;
+    }
+
     // Records `reader` as a deferred product that reads this storage.
     void add_reader(const std::shared_ptr<HipStorage>& reader) {
         std::lock_guard<std::recursive_mutex> lock(state_mutex());
@@ -176,6 +183,7 @@ private:
 };
 
 constexpr std::size_t kHostKeptElements = 16;
+constexpr int kMaxDeferredDepth = 16;
 
 const HipStorage& as_hip(const Storage& s) {
     const auto* h = dynamic_cast<const HipStorage*>(&s);
@@ -442,7 +450,12 @@ std::shared_ptr<Storage> HipBackend::matmul_deferred(const std::shared_ptr<Stora
     if (!ha || !hb) throw std::invalid_argument("expected HIP storage");
     if (a_offset + m * k > ha->size() || b_offset + k * n > hb->size())
         throw std::out_of_range("HIP matmul operand exceeds storage");
+    // Chains of products nobody reads are cut every kMaxDeferredDepth links,
+    // so that computing one never recurses deeper than that.
+    if (ha->pending_depth() >= kMaxDeferredDepth) (void)ha->ptr();
+    if (hb->pending_depth() >= kMaxDeferredDepth) (void)hb->ptr();
     DeferredProduct d;
+    d.depth = 1 + std::max(ha->pending_depth(), hb->pending_depth());
     d.a = ha;
     d.b = hb;
     d.a_offset = a_offset;
@@ -470,6 +483,8 @@ std::shared_ptr<Storage> HipBackend::add_bias_deferred(const Storage& product, s
     const bool row = (bias_shape == Shape{d->n} || bias_shape == Shape{1, d->n}) &&
                      bias_strides == contiguous_strides(bias_shape) && bias_offset + d->n <= hbias->size();
     if (!row) return nullptr;
+    if (hbias->pending_depth() >= kMaxDeferredDepth) (void)hbias->ptr();
+    d->depth = std::max(d->depth, 1 + hbias->pending_depth());
     d->bias = hbias;
     d->bias_offset = bias_offset;
     auto out = std::make_shared<HipStorage>(d->m * d->n, *d);

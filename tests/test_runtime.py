@@ -462,6 +462,30 @@ def test_deferred_product_shared_reshaped_and_as_a_bias():
 
 
 @hip_only
+def test_partial_in_place_update_of_a_deferred_operand():
+    # The device interface's axpy_inplace may update a range of a storage. A
+    # product still deferred on that storage keeps the old values, and the
+    # storage keeps the elements outside the range.
+    rng = np.random.default_rng(12)
+    xs, ws = rng.standard_normal((5, 6)).astype(np.float32), rng.standard_normal((6, 7)).astype(np.float32)
+    gs = rng.standard_normal(42).astype(np.float32)
+
+    def run():
+        x, w, g = vc.Tensor(xs, device="hip"), vc.Tensor(ws, device="hip"), vc.Tensor(gs, device="hip")
+        p = x @ w
+        vc._vectorcore._axpy_inplace(w, 10, g, 3, 20, -0.5)  # w.flat[10:30] -= 0.5 * g[3:23]
+        return [npy(p), npy(w)]
+
+    eager, deferred = _eager_then_deferred(run)
+    _assert_same_bits(eager, deferred)
+    updated = ws.reshape(-1)[10:30] - np.float32(0.5) * gs[3:23]
+    np.testing.assert_array_equal(deferred[1].reshape(-1)[:10], ws.reshape(-1)[:10])
+    np.testing.assert_array_equal(deferred[1].reshape(-1)[30:], ws.reshape(-1)[30:])
+    np.testing.assert_allclose(deferred[1].reshape(-1)[10:30], updated, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(deferred[0], xs.astype(np.float64) @ ws, rtol=1e-4, atol=1e-4 * np.sqrt(6))
+
+
+@hip_only
 def test_long_chain_of_deferred_products():
     # 3000 products, each of the one before, none read until the end: the
     # chain is computed in bounded pieces and gives the eager bits.

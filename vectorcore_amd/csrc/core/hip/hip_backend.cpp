@@ -52,7 +52,6 @@ struct DeferredProduct {
     std::size_t a_offset = 0, b_offset = 0, bias_offset = 0;
     std::size_t m = 0, k = 0, n = 0;
     bool relu = false;
-    int depth = 1;  // 1 + the deepest deferred operand: computing it recurses this deep
 
     [[nodiscard]] bool reads(const HipStorage* s) const { return a.get() == s || b.get() == s || bias.get() == s; }
     void replace(const HipStorage* s, const std::shared_ptr<HipStorage>& with) {
@@ -128,12 +127,6 @@ public:
         return *deferred_;
     }
 
-    // How deep computing this storage would recurse (0: nothing deferred).
-    int pending_depth() const {
-        std::lock_guard<std::recursive_mutex> lock(state_mutex());
-        return deferred_ ? deferred_->depth : 0;
-    }
-
     // Records `reader` as a deferred product that reads this storage.
     void add_reader(const std::shared_ptr<HipStorage>& reader) {
         std::lock_guard<std::recursive_mutex> lock(state_mutex());
@@ -142,14 +135,15 @@ public:
         readers_.push_back(reader);
     }
 
-    // Before an in-place write of this storage. Deferred products that read it
-    // and have not run yet must still see the current contents: the current
-    // buffer moves to a new read-only storage that those products read from,
-    // and this storage continues with a fresh buffer. Returns the storage whose
-    // buffer holds the current contents (this one when nothing was deferred on
-    // it); the caller keeps it alive until the write is enqueued and writes
-    // its result into ptr().
-    std::shared_ptr<const HipStorage> before_write() {
+    // Before an in-place write of elements [offset, offset + count) of this
+    // storage. Deferred products that read it and have not run yet must still
+    // see the current contents: the current buffer moves to a new read-only
+    // storage that those products read from, and this storage continues with
+    // a fresh buffer (holding a copy of the old contents unless the write
+    // covers all of it). Returns the storage whose buffer holds the current
+    // contents (this one when nothing was deferred on it); the caller keeps it
+    // alive until the write is enqueued and writes its result into ptr().
+    std::shared_ptr<const HipStorage> before_write(std::size_t offset, std::size_t count) {
         std::lock_guard<std::recursive_mutex> lock(state_mutex());
         (void)ptr();
         shadow_valid_ = false;
@@ -158,16 +152,26 @@ public:
             auto r = w.lock();
             if (r && r->deferred_ && r->deferred_->reads(this)) waiting.push_back(std::move(r));
         }
-        readers_.clear();
-        if (waiting.empty()) return shared_from_this();
+        if (waiting.empty()) {
+            readers_.clear();
+            return shared_from_this();
+        }
         void* fresh_buffer = nullptr;
         check(vc_hip_alloc(bytes(), &fresh_buffer), "HIP allocation failed");
-        auto previous = std::make_shared<HipStorage>(elements_, ptr_);
+        if (offset != 0 || count != elements_) {
+            const int status = vc_hip_copy(fresh_buffer, ptr_, bytes());
+            if (status != VC_HIP_OK) {
+                (void)vc_hip_release(fresh_buffer);
+                throw_status(status, "HIP copy failed");
+            }
+        }
+        auto previous = std::make_shared<HipStorage>(elements_, ptr_);  // takes over the current buffer
         ptr_ = fresh_buffer;
         for (const auto& r : waiting) {
             r->deferred_->replace(this, previous);
             previous->readers_.push_back(r);
         }
+        readers_.clear();
         return previous;
     }
 
@@ -183,7 +187,6 @@ private:
 };
 
 constexpr std::size_t kHostKeptElements = 16;
-constexpr int kMaxDeferredDepth = 16;
 
 const HipStorage& as_hip(const Storage& s) {
     const auto* h = dynamic_cast<const HipStorage*>(&s);
@@ -416,7 +419,7 @@ void HipBackend::axpy_batch(const std::vector<AxpyItem>& items, float alpha) {
     std::vector<std::size_t> counts;
     for (const AxpyItem& it : items) {
         auto& t = as_hip(*it.target);
-        current.push_back(t.before_write());
+        current.push_back(t.before_write(it.target_offset, it.count));
         if (it.count == 0) continue;
         outputs.push_back(t.ptr() + it.target_offset);
         targets.push_back(current.back()->ptr() + it.target_offset);
@@ -450,12 +453,13 @@ std::shared_ptr<Storage> HipBackend::matmul_deferred(const std::shared_ptr<Stora
     if (!ha || !hb) throw std::invalid_argument("expected HIP storage");
     if (a_offset + m * k > ha->size() || b_offset + k * n > hb->size())
         throw std::out_of_range("HIP matmul operand exceeds storage");
-    // Chains of products nobody reads are cut every kMaxDeferredDepth links,
-    // so that computing one never recurses deeper than that.
-    if (ha->pending_depth() >= kMaxDeferredDepth) (void)ha->ptr();
-    if (hb->pending_depth() >= kMaxDeferredDepth) (void)hb->ptr();
+    // An operand that is itself a deferred product is computed now: nothing
+    // more can join its epilogue once a product reads it, launching it here
+    // lets the device start while the host records the rest, and no record
+    // ever waits on another (computing one never recurses).
+    (void)ha->ptr();
+    (void)hb->ptr();
     DeferredProduct d;
-    d.depth = 1 + std::max(ha->pending_depth(), hb->pending_depth());
     d.a = ha;
     d.b = hb;
     d.a_offset = a_offset;
@@ -483,8 +487,7 @@ std::shared_ptr<Storage> HipBackend::add_bias_deferred(const Storage& product, s
     const bool row = (bias_shape == Shape{d->n} || bias_shape == Shape{1, d->n}) &&
                      bias_strides == contiguous_strides(bias_shape) && bias_offset + d->n <= hbias->size();
     if (!row) return nullptr;
-    if (hbias->pending_depth() >= kMaxDeferredDepth) (void)hbias->ptr();
-    d->depth = std::max(d->depth, 1 + hbias->pending_depth());
+    (void)hbias->ptr();  // a deferred bias is computed now, as a product's operands are
     d->bias = hbias;
     d->bias_offset = bias_offset;
     auto out = std::make_shared<HipStorage>(d->m * d->n, *d);

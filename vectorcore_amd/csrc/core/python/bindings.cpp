@@ -2,6 +2,7 @@
 // module (python/bindings.cpp) with "hip" accepted as a device, plus hip
 // diagnostics (pool statistics, per-launch profiler).
 #include "vectorcore/vectorcore.hpp"
+#include "vectorcore/detail/tensor_impl.hpp"
 
 #include "vc_hip.h"
 
@@ -213,6 +214,21 @@ PYBIND11_MODULE(_vectorcore, m) {
             check(vc_hip_profile_enable(enable ? 1 : 0));
         },
         py::arg("enable"), py::arg("labels") = py::none());
+    m.def(
+        "_axpy_inplace",
+        [](Tensor& target, std::size_t target_offset, const Tensor& source, std::size_t source_offset,
+           std::size_t count, float alpha) {
+            if (target.device() != Device::hip() || source.device() != Device::hip())
+                throw std::invalid_argument("_axpy_inplace takes hip tensors");
+            auto& storage = *target.impl()->storage;
+            HipBackend::instance().axpy_inplace(storage, target.impl()->offset + target_offset, *source.impl()->storage,
+                                                source.impl()->offset + source_offset, count, alpha);
+            storage.bump_version();
+        },
+        py::arg("target"), py::arg("target_offset"), py::arg("source"), py::arg("source_offset"), py::arg("count"),
+        py::arg("alpha"),
+        "HipBackend::axpy_inplace on a range of two hip tensors' storages (the device interface's in-place "
+        "update, for tests).");
     m.def(
         "hip_defer_products",
         [](std::optional<bool> enable) {

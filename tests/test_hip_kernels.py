@@ -110,11 +110,28 @@ def test_gemm_relu_mask_is_gemm_then_relu_backward_bitexact():
             assert (fused.numpy() == 0).any() and (fused.numpy() != 0).any()
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (300, 513, 257), (129, 64, 4100), (64, 4096, 64), (256, 2048, 384)])
+def test_large_nn_product_runs_as_nt_on_a_transposed_copy_with_the_same_bits():
+    """From 4096 rows an NN product transposes B and runs the NT kernel; the
+    LDS tiles, and so the bits, are those of NN on B as stored. Shapes below
+    and above the threshold, with edges that are not multiples of the tile."""
+    rng = np.random.default_rng(31)
+    for (m, k, n) in ((4100, 516, 132), (4095, 516, 132), (8192, 1024, 1000)):
+        a = rng.uniform(-1, 1, size=(m, k)).astype(np.float32)
+        b = rng.uniform(-1, 1, size=(k, n)).astype(np.float32)
+        nn = run_gemm(a, b, m, k, n, 0, 0)[0]
+        nt = run_gemm(a, np.ascontiguousarray(b.T), m, k, n, 0, 1)[0]
+        np.testing.assert_array_equal(nn, nt, err_msg=f"{m}x{k}x{n}")
+        rows = rng.choice(m, 64, replace=False)
+        np.testing.assert_allclose(nn[rows], K.matmul2d(a[rows], b), rtol=1e-4, atol=1e-4 * np.sqrt(k))
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (300, 513, 257), (129, 64, 4100), (64, 4096, 64), (256, 2048, 384),
+                                   (4100, 516, 132)])
 def test_matmul_bias_relu_is_product_then_add_then_relu_bitexact(m, k, n):
     # The fused epilogue against the unfused product followed by the row add
     # and ReLU in fp32 (x > 0 ? x : 0). (64, 4096, 64) splits K, so the
-    # epilogue runs in the split combine.
+    # epilogue runs in the split combine; (4100, 516, 132) takes the
+    # transposed-B route of large products.
     rng = np.random.default_rng(m + k + n)
     a = rng.standard_normal((m, k)).astype(np.float32)
     b = rng.standard_normal((k, n)).astype(np.float32)

@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <limits>
+#include <optional>
 #include <vector>
 
 namespace vchip {
@@ -45,6 +46,10 @@ constexpr int kThreads = 256;
 constexpr int kPadK = 4;                     // LDS row padding
 constexpr int kLdsTile = BM * (BK + kPadK);  // floats per operand tile: [128][32 + 4], k-contiguous
 constexpr int kGroupM = 8;
+#ifndef VC_NN_VIA_NT_MIN_ROWS
+#define VC_NN_VIA_NT_MIN_ROWS 4096
+#endif
+constexpr int64_t kNnViaNtMinRows = VC_NN_VIA_NT_MIN_ROWS;
 constexpr int kXcds = 8;
 
 struct GemmArgs {
@@ -434,6 +439,36 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
     }
 }
 
+// out [cols][rows] = in [rows][cols] transposed, both row-major with rows and
+// cols multiples of 4: 64 x 64 tiles through LDS, 16-byte loads and stores.
+// The padded row (65 floats) keeps both LDS passes free of bank conflicts.
+__global__ __launch_bounds__(256) void transpose64_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                                          int64_t rows, int64_t cols) {
+    __shared__ float tile[64][65];
+    const int64_t r0 = int64_t(blockIdx.y) * 64, c0 = int64_t(blockIdx.x) * 64;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = (t >> 4) + 16 * i, c = (t & 15) * 4;
+        if (r0 + r < rows && c0 + c < cols) {
+            const f4 v = *reinterpret_cast<const f4*>(in + (r0 + r) * cols + c0 + c);
+            tile[r][c] = v.x;
+            tile[r][c + 1] = v.y;
+            tile[r][c + 2] = v.z;
+            tile[r][c + 3] = v.w;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = (t >> 4) + 16 * i, r = (t & 15) * 4;
+        if (c0 + c < cols && r0 + r < rows) {
+            const f4 v{tile[r][c], tile[r + 1][c], tile[r + 2][c], tile[r + 3][c]};
+            *reinterpret_cast<f4*>(out + (c0 + c) * rows + r0 + r) = v;
+        }
+    }
+}
+
 // Portable LDS-tiled FMA kernel (VECTORCORE_HIP_GEMM=simple): 16 x 16 outputs
 // per 256-thread workgroup, one per thread.
 template <bool TA, bool TB>
@@ -487,11 +522,29 @@ const char* variant_label(bool ta, bool tb) {
 // offsets: nullptr for the affine mode (a_bstride / b_bstride).
 void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t a_bstride,
           int64_t b_bstride, const std::vector<int64_t>* offsets, int64_t reduce, int64_t a_rstride, int64_t b_rstride,
-          bool ta, bool tb, const float* relu_mask = nullptr, const float* bias = nullptr, bool relu = false) {
+          bool ta, bool tb, const float* relu_mask = nullptr, const float* bias = nullptr, bool relu = false,
+          bool in_caller_scope = false) {
     Device& d = require_device();
     if (M < 0 || N < 0 || K < 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "negative matrix dimension");
     if (M == 0 || N == 0 || batch == 0) return;
     if (!a || !b || !c) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul: null buffer");
+    // A single large NN product runs as NT on a transposed copy of B: the
+    // kernel is ~3.5% faster when both operands are contiguous along k, which
+    // outweighs the copy (2 K N floats of traffic) once M >= 4096. The LDS
+    // tiles, and so the bits, are those of the NN kernel.
+    if (!ta && !tb && batch == 1 && reduce == 1 && !d.simple_gemm && M >= kNnViaNtMinRows && N % 4 == 0 &&
+        K % 4 == 0 && aligned16(a) && aligned16(b) && !relu_mask) {
+        Profiled prof("gemm_nn", 2.0 * double(M) * double(N) * double(K),
+                      4.0 * double(M * K + 2 * K * N + M * N) + (bias ? 4.0 * double(N) : 0.0));
+        Scratch bt(size_t(K * N) * sizeof(float));
+        launch(transpose64_kernel, dim3(unsigned((N + 63) / 64), unsigned((K + 63) / 64)), dim3(256), 0, d.stream, b,
+               bt.as<float>(), K, N);
+        after_launch("gemm_nn");
+        // Inside this scope: the transpose and the product are timed together.
+        gemm(a, bt.as<float>(), c, M, N, K, 1, 0, 0, nullptr, 1, 0, 0, false, true, nullptr, bias, relu, true);
+        prof.done();
+        return;
+    }
     const int64_t tiles_m_simple = (M + 15) / 16, tiles_n_simple = (N + 15) / 16;
     const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const bool simple = d.simple_gemm;
@@ -567,7 +620,8 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     const double bytes =
         4.0 * (double(M * K + K * N) * double(reduce) + double(M * N) * (relu_mask ? 2.0 : 1.0)) * double(batch) +
         (bias ? 4.0 * double(N) : 0.0);
-    Profiled prof(label, flops, bytes);
+    std::optional<Profiled> prof;
+    if (!in_caller_scope) prof.emplace(label, flops, bytes);
     if (ta && tb) launch_variant<true, true>(args, vec, simple, grid, d.stream);
     else if (ta) launch_variant<true, false>(args, vec, simple, grid, d.stream);
     else if (tb) launch_variant<false, true>(args, vec, simple, grid, d.stream);
@@ -580,7 +634,7 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
                            args.relu);
     }
     after_launch(label);
-    prof.done();
+    if (prof) prof->done();
 }
 
 // Per-batch offsets as the reference passes them: affine ones (the common

@@ -144,15 +144,16 @@ int vc_hip_div_backward(const float* grad, const float* a, const size_t* a_shape
 int vc_hip_matmul(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
                   const size_t* a_offsets, const size_t* b_offsets, size_t batch, int trans_a, int trans_b);
 /* vc_hip_matmul followed by the ReLU backward rule in the same kernel:
- * c = (op(a) @ op(b)) * [relu_input > 0], relu_input laid out like c
- * ([batch][m][n], contiguous). The product of the two steps is the same bits as
- * vc_hip_matmul then vc_hip_relu_backward. No counterpart in the reference: it
+ * c = (op(a) @ op(b)) * [mask > 0], mask laid out like c ([batch][m][n],
+ * contiguous): the ReLU's input or its output, which are positive at the same
+ * places. The product of the two steps is the same bits as vc_hip_matmul then
+ * vc_hip_relu_backward. No counterpart in the reference: it
  * fuses src/ops.cpp:395-403 into the product (src/ops.cpp:252-260) that
  * produces the ReLU's upstream gradient, when the autograd engine finds that
  * product to be the ReLU output's only consumer. */
 int vc_hip_matmul_relu_mask(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
                             const size_t* a_offsets, const size_t* b_offsets, size_t batch, int trans_a, int trans_b,
-                            const float* relu_input);
+                            const float* mask);
 /* A forward layer in one kernel: c = a @ b (+ bias[column]) (then ReLU),
  * a [m][k], b [k][n], bias [n] or null, all contiguous; relu nonzero applies
  * x > 0 ? x : 0 after the bias. The same bits as vc_hip_matmul, then the

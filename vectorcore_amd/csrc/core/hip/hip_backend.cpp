@@ -324,8 +324,8 @@ std::shared_ptr<Storage> HipBackend::matmul_relu_mask(const Storage& a, std::siz
                                                       std::size_t b_offset, std::size_t m, std::size_t k, std::size_t n,
                                                       const std::vector<std::size_t>& a_offsets,
                                                       const std::vector<std::size_t>& b_offsets, bool trans_a,
-                                                      bool trans_b, const Storage& relu_input,
-                                                      std::size_t relu_offset) {
+                                                      bool trans_b, const Storage& mask,
+                                                      std::size_t mask_offset) {
     require(*this);
     if (a_offsets.size() != b_offsets.size() || a_offsets.empty())
         throw std::invalid_argument("HIP matmul needs one A and B offset per batch");
@@ -338,7 +338,7 @@ std::shared_ptr<Storage> HipBackend::matmul_relu_mask(const Storage& a, std::siz
     }
     check(vc_hip_matmul_relu_mask(dptr(a, a_offset), dptr(b, b_offset), out->ptr(), m, k, n, a_offsets.data(),
                                   b_offsets.data(), batch, trans_a ? 1 : 0, trans_b ? 1 : 0,
-                                  dptr(relu_input, relu_offset)),
+                                  dptr(mask, mask_offset)),
           "HIP matmul failed");
     return out;
 }

@@ -46,13 +46,14 @@ public:
                                                   const std::vector<std::size_t>& b_offsets, bool trans_a,
                                                   bool trans_b);
     // matmul() followed by the ReLU backward rule in the same kernel: the output
-    // is multiplied by [relu_input > 0] (relu_input laid out like the output).
+    // is multiplied by [mask > 0] (mask: the ReLU's input or output, laid out
+    // like the product).
     [[nodiscard]] std::shared_ptr<Storage> matmul_relu_mask(const Storage& a, std::size_t a_offset, const Storage& b,
                                                             std::size_t b_offset, std::size_t m, std::size_t k,
                                                             std::size_t n, const std::vector<std::size_t>& a_offsets,
                                                             const std::vector<std::size_t>& b_offsets, bool trans_a,
-                                                            bool trans_b, const Storage& relu_input,
-                                                            std::size_t relu_offset);
+                                                            bool trans_b, const Storage& mask,
+                                                            std::size_t mask_offset);
     [[nodiscard]] std::shared_ptr<Storage> transpose_last2(const Storage& input, std::size_t offset, std::size_t batch,
                                                            std::size_t rows, std::size_t cols);
     [[nodiscard]] std::shared_ptr<Storage> reduce_sum(const Storage& input, std::size_t offset, std::size_t count);

@@ -175,12 +175,12 @@ MatmulPlan plan_matmul(const Tensor& a, const Tensor& b, bool trans_a, bool tran
 
 // op(A) @ op(B) without a gradient rule (transposes read in place).
 Tensor matmul_kernel(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b,
-                     const Tensor* relu_input = nullptr) {
+                     const Tensor* relu_mask = nullptr) {
     require_same_device(a, b);
     const MatmulPlan p = plan_matmul(a, b, trans_a, trans_b);
-    if (relu_input) {  // hip only: the product times [relu_input > 0], relu_input shaped like the product
+    if (relu_mask) {  // hip only: the product times [relu_mask > 0], relu_mask shaped like the product
         auto s = hip().matmul_relu_mask(st(a), off(a), st(b), off(b), p.m, p.k, p.n, p.a_offsets, p.b_offsets,
-                                        trans_a, trans_b, st(*relu_input), off(*relu_input));
+                                        trans_a, trans_b, st(*relu_mask), off(*relu_mask));
         Shape out_shape = p.out_batch;
         out_shape.push_back(p.m);
         out_shape.push_back(p.n);

@@ -676,10 +676,10 @@ int vc_hip_matmul(const float* a, const float* b, float* c, size_t m, size_t k, 
 
 int vc_hip_matmul_relu_mask(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
                             const size_t* a_offsets, const size_t* b_offsets, size_t batch, int trans_a, int trans_b,
-                            const float* relu_input) {
+                            const float* mask) {
     return guard([&] {
-        if (!relu_input) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask: null ReLU input");
-        matmul_offsets(a, b, c, m, k, n, a_offsets, b_offsets, batch, trans_a, trans_b, relu_input);
+        if (!mask) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask: null mask");
+        matmul_offsets(a, b, c, m, k, n, a_offsets, b_offsets, batch, trans_a, trans_b, mask);
     });
 }
 

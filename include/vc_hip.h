@@ -198,6 +198,11 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
  * scalar (the upstream gradient of the loss). */
 int vc_hip_xent_backward(const float* logits, const int32_t* targets, const float* row_stats,
                          const float* grad_loss, size_t rows, size_t classes, float* grad_logits);
+/* vc_hip_xent_backward with the upstream gradient passed by value. No
+ * counterpart in the reference: loss.backward() seeds the loss with a host
+ * value (src/tensor.cpp:244-249), which then needs no upload. */
+int vc_hip_xent_backward_value(const float* logits, const int32_t* targets, const float* row_stats,
+                               float grad_loss, size_t rows, size_t classes, float* grad_logits);
 
 /* ---- measurement ------------------------------------------------------------- */
 /* When enabled, the kernels of each labelled entry-point call carry HIP

@@ -391,6 +391,23 @@ def test_cross_entropy_against_oracle(rows, classes):
     np.testing.assert_allclose(grad, t.grad.data, rtol=1e-5, atol=1e-9)
 
 
+def test_cross_entropy_backward_with_the_seed_by_value_is_bitexact():
+    xe = W.xent(rows=300, classes=1000, seed=9)
+    logits, targets = xe["logits"], xe["targets"].astype(np.int32)
+    rows, classes = logits.shape
+    dl, dt = C.Buffer.of(logits), C.Buffer.of(targets, dtype=np.int32)
+    stats, loss = C.Buffer((rows, 2)), C.Buffer((1,))
+    C.check(C.lib().vc_hip_xent_forward(dl.ptr, dt.ptr, rows, classes, stats.ptr, loss.ptr))
+    for seed in (1.0, 0.37, -2.5):
+        by_ptr, by_value = C.Buffer(logits.shape), C.Buffer(logits.shape)
+        dseed = C.Buffer.of(np.array([seed], np.float32))
+        C.check(C.lib().vc_hip_xent_backward(dl.ptr, dt.ptr, stats.ptr, dseed.ptr, rows, classes, by_ptr.ptr))
+        C.check(C.lib().vc_hip_xent_backward_value(dl.ptr, dt.ptr, stats.ptr, ctypes.c_float(seed), rows, classes,
+                                                   by_value.ptr))
+        np.testing.assert_array_equal(by_value.numpy(), by_ptr.numpy())
+    assert C.lib().vc_hip_xent_backward(dl.ptr, dt.ptr, stats.ptr, None, rows, classes, by_ptr.ptr) != 0
+
+
 def _special_rows(classes, rng):
     """Rows that exercise the max and non-finite rules, with their targets."""
     base = lambda: -np.abs(rng.standard_normal(classes)).astype(np.float32) - 0.5

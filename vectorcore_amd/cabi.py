@@ -60,6 +60,7 @@ _SIGNATURES = {
     "vc_hip_scatter_axis": ([_vp, _vp, _vp, _sz, _sz, _sz], _i),
     "vc_hip_xent_forward": ([_vp, _vp, _sz, _sz, _vp, _vp], _i),
     "vc_hip_xent_backward": ([_vp, _vp, _vp, _vp, _sz, _sz, _vp], _i),
+    "vc_hip_xent_backward_value": ([_vp, _vp, _vp, _f, _sz, _sz, _vp], _i),
     "vc_hip_profile_enable": ([_i], _i),
     "vc_hip_profile_labels": ([ctypes.c_char_p], _i),
     "vc_hip_profile_reset": ([], _i),

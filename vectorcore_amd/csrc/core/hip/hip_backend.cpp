@@ -606,10 +606,15 @@ std::shared_ptr<Storage> HipBackend::cross_entropy_backward(const Storage& logit
                                                             std::size_t rows, std::size_t classes) {
     require(*this);
     auto out = fresh(rows * classes);
-    check(vc_hip_xent_backward(dptr(logits, logits_offset),
-                               reinterpret_cast<const std::int32_t*>(as_hip(targets).ptr()), as_hip(row_stats).ptr(),
-                               dptr(grad_loss, grad_offset), rows, classes, out->ptr()),
-          "HIP cross-entropy backward failed");
+    const auto* t = reinterpret_cast<const std::int32_t*>(as_hip(targets).ptr());
+    // backward()'s seed is a host-known scalar: pass its value, no upload.
+    const std::optional<float> seed = grad_offset == 0 ? hip_host_scalar(grad_loss) : std::nullopt;
+    const int status =
+        seed ? vc_hip_xent_backward_value(dptr(logits, logits_offset), t, as_hip(row_stats).ptr(), *seed, rows, classes,
+                                          out->ptr())
+             : vc_hip_xent_backward(dptr(logits, logits_offset), t, as_hip(row_stats).ptr(),
+                                    dptr(grad_loss, grad_offset), rows, classes, out->ptr());
+    check(status, "HIP cross-entropy backward failed");
     return out;
 }
 

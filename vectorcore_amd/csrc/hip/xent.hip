@@ -282,12 +282,12 @@ struct NegateDivide {
 template <bool Vec>
 __global__ __launch_bounds__(kBlock) void xent_backward_kernel(const float* __restrict__ x, const int* __restrict__ targets,
                                                                const float* __restrict__ stats,
-                                                               const float* __restrict__ grad_loss, int64_t rows,
-                                                               int64_t len, float* __restrict__ dx) {
+                                                               const float* __restrict__ grad_loss, float grad_value,
+                                                               int64_t rows, int64_t len, float* __restrict__ dx) {
     const int lane = threadIdx.x % kWave;
     const int64_t r = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
     if (r >= rows) return;
-    const float c = grad_loss[0] / float(rows);
+    const float c = (grad_loss ? grad_loss[0] : grad_value) / float(rows);
     const float m = stats[2 * r], s = stats[2 * r + 1];
     const float scale = c / s;
     const float neg_c = -c;
@@ -307,6 +307,25 @@ __global__ __launch_bounds__(kBlock) void xent_backward_kernel(const float* __re
     } else {
         for (int64_t a = lane; a < len; a += kWave) out[a] = scale * expf(row[a] - m) + (a == t ? neg_c : -0.0f);
     }
+}
+
+void xent_backward(const float* logits, const int32_t* targets, const float* row_stats, const float* grad_loss,
+                   float grad_value, size_t rows, size_t classes, float* grad_logits) {
+    Device& d = require_device();
+    if (rows == 0 || classes == 0) return;
+    if (classes > size_t(std::numeric_limits<int>::max())) fail(VC_HIP_ERR_OVERFLOW, "too many classes");
+    const int64_t R = int64_t(rows), C = int64_t(classes);
+    const bool vec = C % 4 == 0 && aligned16(logits) && aligned16(grad_logits);
+    const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
+    Profiled p("xent_backward", 0.0, 8.0 * double(R * C) + 12.0 * double(R));
+    if (vec)
+        launch(xent_backward_kernel<true>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, row_stats, grad_loss,
+               grad_value, R, C, grad_logits);
+    else
+        launch(xent_backward_kernel<false>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, row_stats,
+               grad_loss, grad_value, R, C, grad_logits);
+    after_launch("xent_backward");
+    p.done();
 }
 
 }  // namespace
@@ -369,22 +388,14 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
 int vc_hip_xent_backward(const float* logits, const int32_t* targets, const float* row_stats, const float* grad_loss,
                          size_t rows, size_t classes, float* grad_logits) {
     return guard([&] {
-        Device& d = require_device();
-        if (rows == 0 || classes == 0) return;
-        if (classes > size_t(std::numeric_limits<int>::max())) fail(VC_HIP_ERR_OVERFLOW, "too many classes");
-        const int64_t R = int64_t(rows), C = int64_t(classes);
-        const bool vec = C % 4 == 0 && aligned16(logits) && aligned16(grad_logits);
-        const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
-        Profiled p("xent_backward", 0.0, 8.0 * double(R * C) + 12.0 * double(R));
-        if (vec)
-            launch(xent_backward_kernel<true>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets, row_stats,
-                               grad_loss, R, C, grad_logits);
-        else
-            launch(xent_backward_kernel<false>, dim3(grid), dim3(kBlock), 0, d.stream, logits, targets,
-                               row_stats, grad_loss, R, C, grad_logits);
-        after_launch("xent_backward");
-        p.done();
+        if (!grad_loss) fail(VC_HIP_ERR_INVALID_ARGUMENT, "xent_backward: null grad_loss");
+        xent_backward(logits, targets, row_stats, grad_loss, 0.0f, rows, classes, grad_logits);
     });
+}
+
+int vc_hip_xent_backward_value(const float* logits, const int32_t* targets, const float* row_stats, float grad_loss,
+                               size_t rows, size_t classes, float* grad_logits) {
+    return guard([&] { xent_backward(logits, targets, row_stats, nullptr, grad_loss, rows, classes, grad_logits); });
 }
 
 }  // extern "C"

@@ -50,6 +50,8 @@ constexpr int kGroupM = 8;
 #define VC_NN_VIA_NT_MIN_ROWS 4096
 #endif
 constexpr int64_t kNnViaNtMinRows = VC_NN_VIA_NT_MIN_ROWS;
+constexpr int64_t kTinyTiles = 8;  // outputs of at most this many tiles split K finely
+constexpr double kTinyMacs = 1048576.0;
 constexpr int kXcds = 8;
 
 struct GemmArgs {
@@ -547,7 +549,11 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     }
     const int64_t tiles_m_simple = (M + 15) / 16, tiles_n_simple = (N + 15) / 16;
     const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    const bool simple = d.simple_gemm;
+    // Tiny products (<= 2^20 multiply-adds, K <= 128) run on the FMA kernel: a
+    // 128 x 128 MFMA tile there is mostly padding, and its fixed latency
+    // (~8 us) is several times the FMA kernel's whole run.
+    const bool simple =
+        d.simple_gemm || (double(M) * double(N) * double(K) * double(batch) * double(reduce) <= kTinyMacs && K <= 128);
     const int64_t tiles = simple ? tiles_m_simple * tiles_n_simple : tiles_m * tiles_n;
     if (tiles > std::numeric_limits<int>::max() / 2) fail(VC_HIP_ERR_OVERFLOW, "matmul output has too many tiles");
     // Byte offsets relative to a tile origin are 32-bit: 128 rows of any
@@ -589,9 +595,10 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     }
     // Split the work when the output has fewer tiles than two workgroups per
     // CU: a batch reduction (reduce > 1) splits into ranges of r, a long K into
-    // ranges of at least 32 slices (at most 4). Each split accumulates into its
-    // own partial matrix and a second pass sums the partials in split order
-    // (deterministic).
+    // ranges of at least 32 slices (at most 4), and the K of a tiny output
+    // (<= kTinyTiles tiles) into up to 32 ranges. Each split accumulates into
+    // its own partial matrix and a second pass sums the partials in split
+    // order (deterministic). No split range is empty.
     const int kt_total = int((K + BK - 1) / BK);
     int splits = 1;
     int64_t r_per_split = reduce;
@@ -600,11 +607,17 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
         if (reduce > 1) {
             r_per_split = (reduce + std::min(want, reduce) - 1) / std::min(want, reduce);
             splits = int((reduce + r_per_split - 1) / r_per_split);
+        } else if (tiles * batch <= kTinyTiles && kt_total >= 4) {
+            // A handful of output tiles: one workgroup's K loop is a chain of
+            // ~1.7 us steps, so split K as far as 32 ways (one slice or more each).
+            splits = std::min(kt_total, 32);
         } else if (kt_total >= 64) {
             splits = int(std::min<int64_t>(want, 4));
             splits = std::min(splits, kt_total / 32);
         }
     }
+    if (reduce == 1 && splits > 1)  // drop the ranges that ceil(kt_total / splits) slices each would leave empty
+        splits = (kt_total + (kt_total + splits - 1) / splits - 1) / ((kt_total + splits - 1) / splits);
     if (batch * splits > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, "matmul batch too large");
     args.splits = splits;
     args.kt_per_split = (kt_total + splits - 1) / splits;

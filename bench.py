@@ -153,15 +153,21 @@ def _median_ms(fn, reps):
     return statistics.median(times)
 
 
-def _profiled(vc, fn, labels=None):
-    """Per-label kernel aggregates of one call of fn (events on the kernels' dispatches)."""
+def _profiled(vc, fn, labels=None, repeats=5, setup=None):
+    """Per-label kernel aggregates of one call of fn (events on the kernels'
+    dispatches), averaged over `repeats` calls; `setup` runs untimed before each."""
     vc.synchronize()
-    vc.hip_profile(True, labels=labels)
     vc.hip_profile_reset()
-    fn()
+    for _ in range(repeats):
+        if setup:
+            setup()
+            vc.synchronize()
+        vc.hip_profile(True, labels=labels)
+        fn()
+        vc.hip_profile(False)
     out = vc.hip_profile_read()
-    vc.hip_profile(False)
-    return out
+    return {k: {f: (v[f] / repeats if f in ("ms", "flops", "bytes", "launches") else v[f]) for f in v}
+            for k, v in out.items()}
 
 
 def config_measurements(cpu: bool):
@@ -244,8 +250,12 @@ def config_measurements(cpu: bool):
         vc.synchronize()
 
     forward(); backward(); vc.zero_grad([x, bias])
-    forward()
-    prof = _profiled(vc, backward)
+
+    def fresh_forward():
+        vc.zero_grad([x, bias])
+        forward()
+
+    prof = _profiled(vc, backward, setup=fresh_forward)
     vc.zero_grad([x, bias])
     kms = sum(v["ms"] for v in prof.values())
     kbytes = sum(v["bytes"] for v in prof.values())

@@ -82,6 +82,18 @@ int vc_hip_upload(void* dst, const void* src, size_t bytes);
 int vc_hip_download(void* dst, const void* src, size_t bytes);
 /* Device-to-device copy on the library stream. */
 int vc_hip_copy(void* dst, const void* src, size_t bytes);
+/* A one-element value published to host memory without a full
+ * synchronisation: vc_hip_mirror_scalar enqueues, in stream order, a copy of
+ * *device_value into a pinned host slot and returns a handle;
+ * vc_hip_mirror_read waits until the stream has reached that copy (not for
+ * the work enqueued after it) and returns the value; vc_hip_mirror_release
+ * returns the slot. No counterpart in the reference, whose download
+ * (metal_backend.mm:198-211) waits for the whole queue: it lets loss.item()
+ * return while the backward pass and the optimizer step still run. */
+typedef struct vc_hip_mirror vc_hip_mirror;
+int vc_hip_mirror_scalar(const float* device_value, vc_hip_mirror** out);
+int vc_hip_mirror_read(vc_hip_mirror* mirror, float* value);
+int vc_hip_mirror_release(vc_hip_mirror* mirror);
 /* MetalBackend::synchronize (metal_backend.hpp:55): waits and reports any
  * asynchronous device error. */
 int vc_hip_synchronize(void);

@@ -462,6 +462,23 @@ def test_cross_entropy_special_values_match_the_oracle(classes):
     np.testing.assert_allclose(grad, ref.grad.data, rtol=1e-5, atol=1e-9)
 
 
+def test_scalar_mirror_publishes_the_value_at_its_point_in_the_stream():
+    x = C.Buffer.of(np.array([3.25], np.float32))
+    m = ctypes.c_void_p()
+    C.check(C.lib().vc_hip_mirror_scalar(x.ptr, ctypes.byref(m)))
+    C.check(C.lib().vc_hip_fill(x.ptr, 1, ctypes.c_float(-7.0)))  # enqueued after the mirror's copy
+    big = C.Buffer((1 << 22,))
+    C.check(C.lib().vc_hip_fill(big.ptr, 1 << 22, ctypes.c_float(1.0)))
+    v = ctypes.c_float()
+    C.check(C.lib().vc_hip_mirror_read(m, ctypes.byref(v)))
+    assert v.value == 3.25
+    C.check(C.lib().vc_hip_mirror_read(m, ctypes.byref(v)))  # a second read sees the same value
+    assert v.value == 3.25
+    C.check(C.lib().vc_hip_mirror_release(m))
+    assert x.numpy()[0] == -7.0
+    assert C.lib().vc_hip_mirror_scalar(None, ctypes.byref(m)) != 0
+
+
 def test_pool_reuses_released_buffers():
     before = C.pool_stats()
     bufs = [C.Buffer((1 << 20,)) for _ in range(4)]

@@ -813,6 +813,29 @@ def test_hip_sgd_over_many_parameters_matches_one_at_a_time():
 
 
 @hip_only
+def test_hip_loss_item_is_published_without_a_full_synchronisation():
+    # loss.item() reads the value the loss kernel published; later work (the
+    # backward pass, the update) does not change it, and an in-place update of
+    # the loss storage itself withdraws the published value.
+    rng = np.random.default_rng(13)
+    logits = vc.Tensor(rng.standard_normal((64, 10)).astype(np.float32), requires_grad=True, device="hip")
+    targets = list(rng.integers(0, 10, 64))
+    loss = vc.cross_entropy(logits, targets)
+    loss.backward()
+    vc.sgd_step([logits], 0.5)
+    got = loss.item()
+    ref = vc.cross_entropy(vc.Tensor(npy(logits) + 0.5 * npy(logits.grad), device="cpu"), targets).item()
+    assert np.isclose(got, ref, rtol=1e-6)
+    total = (logits * 1.0).sum()
+    assert np.isclose(total.item(), float(npy(logits).astype(np.float64).sum()), rtol=1e-5, atol=1e-4)
+    seed = loss.detach()
+    seed.requires_grad = True
+    (seed * 2.0).sum().backward()
+    vc.sgd_step([seed], 1.0)  # rewrites the loss storage: seed -= 2
+    assert np.isclose(loss.item(), got - 2.0, rtol=1e-6)
+
+
+@hip_only
 def test_hip_gemm_kernel_reported():
     assert vc.hip_gemm_kernel() in ("mfma", "simple")
     assert "gfx950" in vc.hip_device_name()

@@ -35,6 +35,9 @@ _SIGNATURES = {
     "vc_hip_release": ([_vp], _i),
     "vc_hip_upload": ([_vp, _vp, _sz], _i),
     "vc_hip_download": ([_vp, _vp, _sz], _i),
+    "vc_hip_mirror_scalar": ([_vp, ctypes.POINTER(_vp)], _i),
+    "vc_hip_mirror_read": ([_vp, ctypes.POINTER(ctypes.c_float)], _i),
+    "vc_hip_mirror_release": ([_vp], _i),
     "vc_hip_copy": ([_vp, _vp, _sz], _i),
     "vc_hip_synchronize": ([], _i),
     "vc_hip_pool_stats_get": ([_vp], _i),

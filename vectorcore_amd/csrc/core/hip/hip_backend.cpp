@@ -77,6 +77,7 @@ public:
     HipStorage(std::size_t elements, void* buffer) : elements_(elements), ptr_(buffer), shadow_valid_(false) {}
 
     ~HipStorage() override {
+        if (mirror_) (void)vc_hip_mirror_release(mirror_);
         if (ptr_) (void)vc_hip_release(ptr_);
     }
     HipStorage(const HipStorage&) = delete;
@@ -110,13 +111,29 @@ public:
         return std::nullopt;
     }
 
-    // Host copy readable without the device (no synchronisation needed).
+    // Host copy readable without a full synchronisation: the host shadow, or
+    // the published value of a one-element result (waits for its producer only).
     bool host_copy(std::size_t offset, float* dst, std::size_t n) const {
         std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        if (mirror_ && elements_ == 1 && offset == 0 && n == 1) {
+            check(vc_hip_mirror_read(mirror_, dst), "HIP command failed");
+            return true;
+        }
         if (!shadow_valid_ || shadow_.empty()) return false;
         std::copy(shadow_.begin() + static_cast<std::ptrdiff_t>(offset),
                   shadow_.begin() + static_cast<std::ptrdiff_t>(offset + n), dst);
         return true;
+    }
+
+    // Publishes this one-element storage's value, as computed so far in stream
+    // order, for host_copy (vc_hip_mirror_scalar).
+    void publish() {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        if (elements_ != 1) return;
+        vc_hip_mirror* m = nullptr;
+        check(vc_hip_mirror_scalar(ptr(), &m), "HIP launch failed");
+        if (mirror_) (void)vc_hip_mirror_release(mirror_);
+        mirror_ = m;
     }
 
     // The deferred product this storage still has to compute, if any (a copy
@@ -147,6 +164,10 @@ public:
         std::lock_guard<std::recursive_mutex> lock(state_mutex());
         (void)ptr();
         shadow_valid_ = false;
+        if (mirror_) {  // the published value is about to be stale
+            (void)vc_hip_mirror_release(mirror_);
+            mirror_ = nullptr;
+        }
         std::vector<std::shared_ptr<HipStorage>> waiting;
         for (const auto& w : readers_) {
             auto r = w.lock();
@@ -183,6 +204,7 @@ private:
     std::vector<float> shadow_;
     mutable std::unique_ptr<DeferredProduct> deferred_;
     std::vector<std::weak_ptr<HipStorage>> readers_;
+    vc_hip_mirror* mirror_ = nullptr;  // published value of a one-element result
     bool shadow_valid_;
 };
 
@@ -373,6 +395,7 @@ std::shared_ptr<Storage> HipBackend::reduce_sum(const Storage& input, std::size_
     require(*this);
     auto out = fresh(1);
     check(vc_hip_reduce_sum(count ? dptr(input, offset) : nullptr, count, out->ptr()), "HIP sum failed");
+    out->publish();  // item() on the sum then waits for this point of the stream only
     return out;
 }
 
@@ -597,6 +620,7 @@ std::pair<std::shared_ptr<Storage>, std::shared_ptr<Storage>> HipBackend::cross_
     check(vc_hip_xent_forward(dptr(logits, logits_offset), reinterpret_cast<const std::int32_t*>(as_hip(targets).ptr()),
                               rows, classes, stats->ptr(), loss->ptr()),
           "HIP cross-entropy failed");
+    loss->publish();  // loss.item() then waits for the forward only, not the backward and update after it
     return {loss, stats};
 }
 

@@ -5,13 +5,15 @@
 // the pool can be handed out again immediately: any later use is ordered
 // after every earlier one. The host waits only in vc_hip_download and
 // vc_hip_synchronize (and, rarely, when the pinned staging ring or the pool
-// needs memory back).
+// needs memory back), and in vc_hip_mirror_read, which waits for one point of
+// the stream only.
 #include "vc_hip_internal.hpp"
 
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <deque>
+#include <memory>
 #include <unordered_map>
 
 namespace vchip {
@@ -230,6 +232,54 @@ private:
 Staging& staging() {
     static Staging s;
     return s;
+}
+
+// ---- scalar mirrors ---------------------------------------------------------------
+// A one-element device value copied, in stream order, into a pinned host slot by
+// a one-thread kernel whose dispatch carries a completion event. Reading the
+// value waits for that event only, not for the work enqueued after it.
+
+__global__ void mirror_kernel(const float* __restrict__ src, float* __restrict__ dst) {
+    if (threadIdx.x == 0) dst[0] = src[0];
+}
+
+class Mirrors {
+public:
+    vc_hip_mirror* take() {
+        std::lock_guard<std::mutex> lock(mu_);
+        if (free_.empty()) grow();
+        vc_hip_mirror* m = free_.back();
+        free_.pop_back();
+        return m;
+    }
+    void give(vc_hip_mirror* m) {
+        std::lock_guard<std::mutex> lock(mu_);
+        free_.push_back(m);
+    }
+
+private:
+    static constexpr size_t kSlots = 256;
+    void grow() {
+        float* slab = nullptr;
+        check_hip(hipHostMalloc(reinterpret_cast<void**>(&slab), kSlots * sizeof(float), hipHostMallocDefault),
+                  "hipHostMalloc (scalar mirrors)");
+        auto block = std::make_unique<vc_hip_mirror[]>(kSlots);
+        for (size_t i = 0; i < kSlots; ++i) {
+            block[i].host = slab + i;
+            check_hip(hipEventCreate(&block[i].done), "hipEventCreate");
+            free_.push_back(&block[i]);
+        }
+        blocks_.push_back(std::move(block));  // slots and events live until the process ends
+    }
+
+    std::mutex mu_;
+    std::vector<vc_hip_mirror*> free_;
+    std::vector<std::unique_ptr<vc_hip_mirror[]>> blocks_;
+};
+
+Mirrors& mirrors() {
+    static Mirrors m;
+    return m;
 }
 
 // ---- profiler -----------------------------------------------------------------
@@ -489,6 +539,35 @@ int vc_hip_download(void* dst, const void* src, size_t bytes) {
         }
         check_hip(hipStreamSynchronize(d.stream), "HIP command failed");
         staging().on_synchronized();
+    });
+}
+
+int vc_hip_mirror_scalar(const float* device_value, vc_hip_mirror** out) {
+    return guard([&] {
+        Device& d = require_device();
+        if (!device_value || !out) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_mirror_scalar: null pointer");
+        vc_hip_mirror* m = mirrors().take();
+        hipExtLaunchKernelGGL(mirror_kernel, dim3(1), dim3(64), 0, d.stream, nullptr, m->done, 0u, device_value, m->host);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) {
+            mirrors().give(m);
+            fail(VC_HIP_ERR_RUNTIME, std::string("launch of mirror_kernel failed: ") + hipGetErrorString(e));
+        }
+        *out = m;
+    });
+}
+
+int vc_hip_mirror_read(vc_hip_mirror* mirror, float* value) {
+    return guard([&] {
+        if (!mirror || !value) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_mirror_read: null pointer");
+        check_hip(hipEventSynchronize(mirror->done), "HIP command failed");
+        *value = *static_cast<volatile float*>(mirror->host);
+    });
+}
+
+int vc_hip_mirror_release(vc_hip_mirror* mirror) {
+    return guard([&] {
+        if (mirror) mirrors().give(mirror);
     });
 }
 

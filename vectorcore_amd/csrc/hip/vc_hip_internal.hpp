@@ -15,6 +15,13 @@
 
 #include "vc_hip.h"
 
+// A pinned host slot and the event that completes when a value has been
+// copied into it (vc_hip_mirror_scalar).
+struct vc_hip_mirror {
+    float* host;
+    hipEvent_t done;
+};
+
 namespace vchip {
 
 // An error carrying the C-ABI status it maps to.

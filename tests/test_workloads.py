@@ -315,3 +315,35 @@ def test_mlp_train_steps_are_bitwise_reproducible():
     assert l1 == l2 and l1[-1] < l1[0]
     for a, b in zip(p1, p2):
         np.testing.assert_array_equal(a, b)
+
+
+def test_config5_steps_with_and_without_deferred_products_are_bitwise_equal():
+    """The full-size step with its forward products deferred (bias and ReLU in
+    the GEMM epilogue, large products on a transposed B, copy-on-write for the
+    updated weights) against eager products: two steps, bit for bit."""
+    m = W.mlp()
+
+    def run():
+        params = build_mlp(m["weights"], m["biases"])
+        x = H(m["x"])
+        losses = []
+        for _ in range(2):
+            loss = vc.cross_entropy(mlp_logits(params, x), m["targets"])
+            loss.backward()
+            vc.sgd_step(params, m["lr"])
+            vc.zero_grad(params)
+            losses.append(loss.item())
+        return losses, [p.numpy() for p in params]
+
+    previous = vc.hip_defer_products(False)
+    try:
+        eager = run()
+    finally:
+        vc.hip_defer_products(True)
+    try:
+        deferred = run()
+    finally:
+        vc.hip_defer_products(previous)
+    assert eager[0] == deferred[0]
+    for a, b in zip(eager[1], deferred[1]):
+        np.testing.assert_array_equal(a, b)

@@ -223,22 +223,21 @@ __global__ __launch_bounds__(kBlock) void colsum_tile_kernel(const float* __rest
     }
 }
 
-// out[t] = float(sum over segments of part[s][t]), in segment order. Loads are
-// issued eight at a time so a thread is not bound by one load's latency.
+// out[t] = float(sum over segments of part[s][t]), in segment order. All
+// segments' loads are issued before the first add (one memory round trip).
+constexpr int kMaxColSegs = 64;
 __global__ __launch_bounds__(kBlock) void colsum_combine_kernel(const double* __restrict__ part, float* __restrict__ out,
-                                                                int64_t total, int64_t segs) {
+                                                                int64_t total, int segs) {
     const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (t >= total) return;
+    double v[kMaxColSegs];
+#pragma unroll
+    for (int s = 0; s < kMaxColSegs; ++s)
+        if (s < segs) v[s] = part[s * total + t];
     double acc = 0.0;
-    int64_t s = 0;
-    for (; s + 8 <= segs; s += 8) {
-        double v[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = part[(s + k) * total + t];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) acc += v[k];
-    }
-    for (; s < segs; ++s) acc += part[s * total + t];
+    for (int s = 0; s < kMaxColSegs; ++s)
+        if (s < segs) acc += v[s];
     out[t] = float(acc);
 }
 
@@ -325,7 +324,7 @@ void column_sum(Device& d, const float* in, float* out, int64_t outer, int64_t l
     // Segments: a function of the shape only; aim at ~2048 workgroups, at
     // least 64 rows per segment, at most 64 segments.
     int64_t segs = std::max<int64_t>(1, (2048 + blocks_x - 1) / blocks_x);
-    segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / 64), 64});
+    segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / 64), int64_t(kMaxColSegs)});
     const int64_t seg_len = (len + segs - 1) / segs;
     segs = (len + seg_len - 1) / seg_len;
     if (blocks_x > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, "reduction too large");
@@ -340,7 +339,7 @@ void column_sum(Device& d, const float* in, float* out, int64_t outer, int64_t l
                            inner, seg_len, chunks);
     after_launch(label);
     launch(colsum_combine_kernel, dim3(unsigned((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, d.stream,
-                       part.as<double>(), out, total, segs);
+                       part.as<double>(), out, total, int(segs));
     after_launch(label);
 }
 

@@ -190,13 +190,23 @@ __global__ __launch_bounds__(kBlock) void sum_partial_kernel(const float* __rest
 }
 
 // Stage two: out = finish(float(sum of the partials)); thread t takes
-// b = t, t + blockDim, ..., then the fixed workgroup tree.
+// b = t, t + blockDim, ... (eight loads in flight), then the fixed workgroup
+// tree.
 template <class Finish>
 __global__ __launch_bounds__(kBlock) void sum_final_kernel(const double* __restrict__ part, float* __restrict__ out,
                                                            int64_t blocks, Finish finish) {
     __shared__ double lds[kBlock / kWave];
     double acc = 0.0;
-    for (int64_t b = threadIdx.x; b < blocks; b += blockDim.x) acc += part[b];
+    const int64_t step = blockDim.x;
+    int64_t b = threadIdx.x;
+    for (; b + 7 * step < blocks; b += 8 * step) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = part[b + u * step];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; b < blocks; b += step) acc += part[b];
     const double total = block_sum(acc, lds);
     if (threadIdx.x == 0) out[0] = finish(float(total));
 }

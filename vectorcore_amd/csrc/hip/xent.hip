@@ -348,7 +348,9 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
         Profiled p("xent_forward", 0.0, 4.0 * double(R * C) + 4.0 * double(R) + 8.0 * double(R));
         // Rows of up to 4096 classes are held in registers (NV float4 per lane),
-        // with at most 8 wavefronts per SIMD walking the rows.
+        // with at most 8 workgroups per CU walking the rows (5 fit at once at
+        // this kernel's register use; sizing the grid to exactly one resident
+        // round measured the same).
         const int64_t nv = vec ? (C + kWave * 4 - 1) / (kWave * 4) : 0;
         const unsigned cached_grid = unsigned(std::min<int64_t>((R + kRowsPerBlock - 1) / kRowsPerBlock,
                                                                 int64_t(d.cu_count) * 8));

@@ -2,9 +2,9 @@
 
 Bars: bit-exact for indices (argmax), for pure-fp32 elementwise chains and
 for data movement; the reference's own tolerance pairs elsewhere (GEMM:
-rtol 1e-4, atol 1e-4 sqrt(k), tests/python/test_performance_paths.py:43;
-reductions rtol 1e-4 and BASELINE's 1e-4 relative; transcendental
-elementwise results within 1e-5 relative, BASELINE's elementwise bar).
+rtol 1e-4, atol 1e-4 sqrt(k), tests/python/test_performance_paths.py:43);
+reductions within 1e-4 relative; transcendental elementwise results within
+1e-5 relative.
 """
 
 import ctypes

@@ -2,9 +2,9 @@
 (autograd graph, hip device) against the oracle and the reference fixtures.
 
 Tolerances (written per check): bit-exact for argmax; 1e-5 relative for
-elementwise gradients (BASELINE's elementwise bar, with an absolute floor for
-values near zero); 1e-4 relative for GEMM and reduction results (BASELINE's
-GEMM/reduction bar, with the reference's own atol = 1e-4 sqrt(k) for GEMMs).
+elementwise gradients (with an absolute floor for values near zero); 1e-4
+relative for GEMM and reduction results (with the reference's own
+atol = 1e-4 sqrt(k) for GEMMs, tests/python/test_performance_paths.py:43).
 """
 
 import numpy as np

@@ -1,8 +1,8 @@
 """ctypes binding of the C ABI in include/vc_hip.h (libvc_hip.so).
 
-This is the same binding a Python-side FFI of the reference would add (see
-INTEGRATION.md); tests use it to drive every entry point directly. Loading
-fails loudly when the library has not been built.
+This is the same binding a Python-side FFI of the reference would add; tests
+use it to drive every entry point directly. Loading fails loudly when the
+library has not been built.
 """
 
 from __future__ import annotations

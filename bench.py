@@ -184,7 +184,7 @@ def config_measurements(cpu: bool):
         ref = K.Reference() if K.Reference.available() else None
     out = {}
 
-    # C1: spiral classifier train step (launch-bound; no roofline).
+    # Spiral classifier train step (launch-bound; no roofline).
     sp = W.spiral()
     ps = []
     for w, b in zip(sp["weights"], sp["biases"]):
@@ -215,12 +215,12 @@ def config_measurements(cpu: bool):
         net = ref.mlp(sp["weights"], sp["biases"], sp["x"], sp["targets"])
         net.step(sp["lr"])
         c1["cpu_reference_steps_per_s"] = round(1e3 / _median_ms(lambda: net.step(sp["lr"]), 50), 1)
-    out["C1"] = c1
+    out["spiral_train_step"] = c1
 
-    # C2: batched matmul backward, dA = dC B^T (NT) and dB = A^T dC (TN).
+    # Batched matmul backward, dA = dC B^T (NT) and dB = A^T dC (TN).
     bm = W.bmm()
     flops = 2.0 * 8 * 1024 ** 3
-    for name, bkey in (("C2", "b"), ("C2_broadcast_B", "b_shared")):
+    for name, bkey in (("batched_matmul_backward", "b"), ("batched_matmul_backward_broadcast_b", "b_shared")):
         a = vc.Tensor(bm["a"], requires_grad=True, device="hip")
         b = vc.Tensor(bm[bkey], requires_grad=True, device="hip")
         dc = vc.Tensor(bm["dc"], device="hip")
@@ -243,7 +243,7 @@ def config_measurements(cpu: bool):
         out[name] = c2
         del a, b, dc
 
-    # C3: y = sigmoid(relu(x + bias)) * exp(0.1 x); backward for dx, dbias.
+    # Activation chain y = sigmoid(relu(x + bias)) * exp(0.1 x); backward for dx, dbias.
     ac = W.activation()
     x = vc.Tensor(ac["x"], requires_grad=True, device="hip")
     bias = vc.Tensor(ac["bias"], requires_grad=True, device="hip")
@@ -282,10 +282,10 @@ def config_measurements(cpu: bool):
     if ref:
         c3["cpu_reference_ms_forward_backward"] = round(
             _median_ms(lambda: ref.activation_backward(ac["x"], ac["bias"], ac["dy"]), 1), 1)
-    out["C3"] = c3
+    out["activation_backward"] = c3
     del x, bias, dy, holder
 
-    # C4: mean softmax cross-entropy forward + backward, argmax over classes.
+    # Mean softmax cross-entropy forward + backward, argmax over classes.
     xe = W.xent()
     lg = vc.Tensor(xe["logits"], requires_grad=True, device="hip")
     tg = xe["targets"]
@@ -308,7 +308,7 @@ def config_measurements(cpu: bool):
             c4[label] = {"ms": round(v["ms"], 4), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)}
     if ref:
         c4["cpu_reference_ms"] = round(_median_ms(lambda: ref.cross_entropy(xe["logits"], tg), 1), 1)
-    out["C4"] = c4
+    out["cross_entropy"] = c4
     if ref:
         out["cpu_reference_threads"] = ref.threads()
     return out

@@ -317,7 +317,7 @@ def test_mlp_train_steps_are_bitwise_reproducible():
         np.testing.assert_array_equal(a, b)
 
 
-def test_config5_steps_with_and_without_deferred_products_are_bitwise_equal():
+def test_mlp_train_steps_with_and_without_deferred_products_are_bitwise_equal():
     """The full-size step with its forward products deferred (bias and ReLU in
     the GEMM epilogue, large products on a transposed B, copy-on-write for the
     updated weights) against eager products: two steps, bit for bit."""

@@ -337,8 +337,8 @@ def main():
                     help="first stream 256 MiB through a negate kernel (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the data-parallel "
-              "sharding of this workload is a design note, not a launched path)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the data-parallel sharding of "
+              "this workload is a design note, not a launched path)", file=sys.stderr)
         sys.exit(2)
 
     r = gpu_bench(args.steps, args.warmup, args.copy_calibration)

@@ -1,7 +1,7 @@
 #pragma once
 // Devices (API of include/vectorcore/device.hpp) with the MI355X `hip` device
 // added next to `cpu`. METAL is kept so code written for the reference still
-// compiles; this build has no Metal backend and reports it unavailable.
+// compiles; there is no Metal backend here, and it reports itself unavailable.
 #include <string>
 
 namespace vectorcore {

@@ -1,5 +1,5 @@
 #pragma once
-// The reference's Apple Metal device is not part of this build; these keep its
+// The reference's Apple Metal device is not implemented here; these keep its
 // free functions (include/vectorcore/metal_backend.hpp:58-63) with the
 // behaviour the reference has on a machine without Metal.
 #include <string>

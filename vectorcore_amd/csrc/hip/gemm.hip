@@ -533,9 +533,10 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     // A single large NN product runs as NT on a transposed copy of B: the
     // kernel is ~3.5% faster when both operands are contiguous along k, which
     // outweighs the copy (2 K N floats of traffic) once M >= 4096. The LDS
-    // tiles, and so the bits, are those of the NN kernel.
+    // tiles, and so the bits, are those of the NN kernel. (K is bounded by the
+    // transpose's grid: 65535 tiles of 64 rows.)
     if (!ta && !tb && batch == 1 && reduce == 1 && !d.simple_gemm && M >= kNnViaNtMinRows && N % 4 == 0 &&
-        K % 4 == 0 && aligned16(a) && aligned16(b) && !relu_mask) {
+        K % 4 == 0 && K <= int64_t(65535) * 64 && aligned16(a) && aligned16(b) && !relu_mask) {
         Profiled prof("gemm_nn", 2.0 * double(M) * double(N) * double(K),
                       4.0 * double(M * K + 2 * K * N + M * N) + (bias ? 4.0 * double(N) : 0.0));
         Scratch bt(size_t(K * N) * sizeof(float));

@@ -212,14 +212,16 @@ __device__ inline void read_part(const float* __restrict__ lds, int off, int g, 
 // than spilling.
 template <bool TA, bool TB, bool Vec>
 __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmArgs p) {
-    // Two LDS stages. Step kt multiplies out of stage cur while its first k-group
-    // also stores slice kt + 1 (in registers since step kt - 1) into the other
-    // stage and issues the global loads of slice kt + 2 (an m/n-contiguous
-    // operand in the second k-group, after its transposed stores have read all
-    // four slots). Fragments are read one k-group ahead; after the third
-    // group's MFMAs one barrier makes stage cur ^ 1 complete and stage cur
-    // free, and the fourth group's MFMAs overlap the reads of the next step's
-    // first group.
+    // Two LDS stages. Step kt multiplies out of stage cur while its second
+    // k-group also stores slice kt + 1 (in registers since step kt - 1) into
+    // the other stage and issues the global loads of slice kt + 2 (an
+    // m/n-contiguous operand in the third k-group, after its transposed stores
+    // have read all four slots). Storing in the second group rather than the
+    // first lets a tile's first step run a group of MFMAs while slice 1, loaded
+    // just before it, is still arriving. Fragments are read one k-group ahead;
+    // after the third group's MFMAs one barrier makes stage cur ^ 1 complete
+    // and stage cur free, and the fourth group's MFMAs overlap the reads of the
+    // next step's first group.
     __shared__ __attribute__((aligned(16))) float As[2][kLdsTile];
     __shared__ __attribute__((aligned(16))) float Bs[2][kLdsTile];
     constexpr bool AKC = !TA;  // A contiguous along k
@@ -311,16 +313,16 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
                     if (g == BK / 8 - 1) __syncthreads();
 #pragma unroll
                     for (int s = 0; s < 4; ++s) {
-                        // Store q of the next stage at step q of k-group 0. A
+                        // Store q of the next stage at step q of k-group 1. A
                         // k-contiguous operand then reloads slot q right away;
                         // a transposed store reads all four slots, so that
-                        // operand reloads them in k-group 1.
-                        if (g == 0) {
+                        // operand reloads them in k-group 2.
+                        if (g == 1) {
                             store_slot<AKC, Vec>(st_a, a_st, ra, s);
                             store_slot<BKC, Vec>(st_b, b_st, rb, s);
                         }
-                        if (g == (AKC ? 0 : 1)) ra[s] = la.load(sa, kt + 2, s);
-                        if (g == (BKC ? 0 : 1)) rb[s] = lb.load(sb, kt + 2, s);
+                        if (g == (AKC ? 1 : 2)) ra[s] = la.load(sa, kt + 2, s);
+                        if (g == (BKC ? 1 : 2)) rb[s] = lb.load(sb, kt + 2, s);
                         if (g + 1 < BK / 8) {
                             read_part(as, wm, g + 1, lane, s, 0, fa[cb ^ 1]);
                             read_part(bs, wn, g + 1, lane, s, 2, fb[cb ^ 1]);

@@ -68,6 +68,14 @@ const char* vc_hip_last_error(void);
  * "simple" (portable FMA tiles, forced by VECTORCORE_HIP_GEMM=simple),
  * or "unavailable". */
 const char* vc_hip_gemm_kernel(void);
+/* Selects the GEMM kernel for later calls: "mfma" or "simple". The reference
+ * picks its kernel once, from VECTORCORE_METAL_GEMM=tiled
+ * (src/metal/metal_backend.mm:96-100), and re-runs its GEMM tests in a child
+ * process to cover the portable one (tests/python/test_performance_paths.py:
+ * 89-103); this setter lets one process run them on both kernels. Work
+ * already enqueued keeps its kernel. VC_HIP_ERR_INVALID_ARGUMENT for any
+ * other name. */
+int vc_hip_set_gemm_kernel(const char* name);
 
 /* ---- memory (stream-ordered size-class pool) ----------------------------- */
 /* MetalBackend::allocate (metal_backend.hpp:23, metal_backend.mm:161-182). */
@@ -86,7 +94,10 @@ int vc_hip_copy(void* dst, const void* src, size_t bytes);
  * synchronisation: vc_hip_mirror_scalar enqueues, in stream order, a copy of
  * *device_value into a pinned host slot and returns a handle;
  * vc_hip_mirror_read waits until the stream has reached that copy (not for
- * the work enqueued after it) and returns the value; vc_hip_mirror_release
+ * the work enqueued after it), fails with any error the stream has already
+ * recorded, and returns the value (a fault in work still running after the
+ * copy surfaces at the next vc_hip_download or vc_hip_synchronize);
+ * vc_hip_mirror_release
  * returns the slot. No counterpart in the reference, whose download
  * (metal_backend.mm:198-211) waits for the whole queue: it lets loss.item()
  * return while the backward pass and the optimizer step still run. */

@@ -27,6 +27,16 @@ def device():
     C.synchronize()
 
 
+@pytest.fixture(params=["mfma", "simple"])
+def gemm_kernel(request):
+    """Runs a GEMM test on the MFMA kernel and again on the portable FMA kernel
+    (the reference re-runs its matmul tests with its portable kernel forced,
+    tests/python/test_performance_paths.py:89-103)."""
+    with C.gemm_kernel(request.param):
+        assert C.lib().vc_hip_gemm_kernel().decode() == request.param
+        yield request.param
+
+
 def run_gemm(a, b, m, k, n, ta, tb, batch=1, a_offsets=None, b_offsets=None):
     da, db = C.Buffer.of(a), C.Buffer.of(b)
     dc = C.Buffer((batch, m, n))
@@ -37,7 +47,7 @@ def run_gemm(a, b, m, k, n, ta, tb, batch=1, a_offsets=None, b_offsets=None):
 
 
 @pytest.mark.parametrize("m,k,n", GEMM_SHAPES)
-def test_gemm_matches_reference_fixture(golden, m, k, n):
+def test_gemm_matches_reference_fixture(golden, gemm_kernel, m, k, n):
     for ta in (0, 1):
         for tb in (0, 1):
             a, b = gemm_inputs(m, k, n, ta, tb)
@@ -46,9 +56,14 @@ def test_gemm_matches_reference_fixture(golden, m, k, n):
                                        err_msg=f"trans_a={ta} trans_b={tb}")
 
 
-@pytest.mark.parametrize("m,k,n", [(128, 64, 128), (192, 256, 64), (128, 60, 128), (130, 64, 128), (128, 64, 70),
-                                   (257, 129, 383), (512, 1024, 1000), (1, 4096, 3), (1000, 7, 1)])
-def test_gemm_edges_against_oracle(m, k, n):
+# Every shape but the last is above the tiny-product threshold (2^20
+# multiply-adds with K <= 128), so with "mfma" it runs on the MFMA kernel:
+# a whole tile, a partial K slice (60, 129), partial m and n tiles (130, 70,
+# 257, 383), and vector and scalar loads in all four transposes. The last
+# runs on the FMA kernel with either setting.
+@pytest.mark.parametrize("m,k,n", [(256, 64, 128), (192, 256, 64), (256, 60, 128), (130, 64, 128), (256, 64, 70),
+                                   (257, 129, 383), (512, 1024, 1000), (1, 4096, 3), (2000, 7, 129), (1000, 7, 1)])
+def test_gemm_edges_against_oracle(gemm_kernel, m, k, n):
     rng = np.random.default_rng(m * 7 + k * 3 + n)
     for ta in (0, 1):
         for tb in (0, 1):
@@ -58,7 +73,7 @@ def test_gemm_edges_against_oracle(m, k, n):
                                        rtol=1e-4, atol=1e-4 * np.sqrt(k), err_msg=f"trans_a={ta} trans_b={tb}")
 
 
-def test_gemm_batched_offsets_affine_and_table():
+def test_gemm_batched_offsets_affine_and_table(gemm_kernel):
     rng = np.random.default_rng(3)
     m, k, n = 33, 70, 41
     a = rng.standard_normal((4, m, k)).astype(np.float32)
@@ -74,7 +89,7 @@ def test_gemm_batched_offsets_affine_and_table():
         np.testing.assert_allclose(got[z], K.matmul2d(a[z], b[0]), rtol=1e-4, atol=1e-4 * np.sqrt(k))
 
 
-def test_gemm_split_k_long_reductions():
+def test_gemm_split_k_long_reductions(gemm_kernel):
     """Few output tiles and a long K: the K range is split across workgroups
     and the partial products are summed in split order, so results repeat
     bit for bit."""
@@ -90,7 +105,7 @@ def test_gemm_split_k_long_reductions():
             np.testing.assert_array_equal(run_gemm(a, b, m, k, n, ta, tb, batch=batch), got)
 
 
-def test_gemm_relu_mask_is_gemm_then_relu_backward_bitexact():
+def test_gemm_relu_mask_is_gemm_then_relu_backward_bitexact(gemm_kernel):
     """vc_hip_matmul_relu_mask = vc_hip_matmul, then vc_hip_relu_backward with
     the same mask source: same bits, including a split-K shape and a batch."""
     rng = np.random.default_rng(21)
@@ -127,7 +142,7 @@ def test_large_nn_product_runs_as_nt_on_a_transposed_copy_with_the_same_bits():
 
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (300, 513, 257), (129, 64, 4100), (64, 4096, 64), (256, 2048, 384),
                                    (4100, 516, 132)])
-def test_matmul_bias_relu_is_product_then_add_then_relu_bitexact(m, k, n):
+def test_matmul_bias_relu_is_product_then_add_then_relu_bitexact(gemm_kernel, m, k, n):
     # The fused epilogue against the unfused product followed by the row add
     # and ReLU in fp32 (x > 0 ? x : 0). (64, 4096, 64) splits K, so the
     # epilogue runs in the split combine; (4100, 516, 132) takes the
@@ -149,7 +164,7 @@ def test_matmul_bias_relu_is_product_then_add_then_relu_bitexact(m, k, n):
         np.testing.assert_array_equal(dc.numpy(), expected)
 
 
-def test_gemm_batch_reduce_matches_summed_products():
+def test_gemm_batch_reduce_matches_summed_products(gemm_kernel):
     """dB of a batch-broadcast B: sum_z A[z]^T dC[z] in one launch."""
     bm = W.bmm(batch=3, m=96, k=80, n=72, seed=1)
     a, dc = bm["a"], bm["dc"]
@@ -406,6 +421,37 @@ def test_cross_entropy_backward_with_the_seed_by_value_is_bitexact():
                                                    by_value.ptr))
         np.testing.assert_array_equal(by_value.numpy(), by_ptr.numpy())
     assert C.lib().vc_hip_xent_backward(dl.ptr, dt.ptr, stats.ptr, None, rows, classes, by_ptr.ptr) != 0
+
+
+def test_cross_entropy_register_and_streaming_paths_agree():
+    # Aligned rows of 1000 classes take the register-held forward and the
+    # vector backward; the same rows one float off 16-byte alignment take the
+    # streaming forward and the scalar backward. All of them take their
+    # exponentials from one function, so the row maxima agree bit for bit, the
+    # exp-sums (double sums in another lane order) to the last bit of float,
+    # and, given the same row statistics, the gradients bit for bit.
+    xe = W.xent(rows=2000, classes=1000, seed=17)
+    logits, targets = xe["logits"], xe["targets"].astype(np.int32)
+    rows, classes = logits.shape
+    padded = np.concatenate([np.zeros(1, np.float32), logits.reshape(-1)])
+    dl, dpad, dt = C.Buffer.of(logits), C.Buffer.of(padded), C.Buffer.of(targets, dtype=np.int32)
+    shifted = dpad.ptr + 4  # 4 bytes past a pool buffer's 256-byte alignment
+    out = {}
+    for name, ptr in (("registers", dl.ptr), ("streaming", shifted)):
+        stats, loss = C.Buffer((rows, 2)), C.Buffer((1,))
+        C.check(C.lib().vc_hip_xent_forward(ptr, dt.ptr, rows, classes, stats.ptr, loss.ptr))
+        out[name] = (stats, loss.numpy()[0])
+    s_reg, s_str = out["registers"][0].numpy(), out["streaming"][0].numpy()
+    np.testing.assert_array_equal(s_str[:, 0], s_reg[:, 0])
+    np.testing.assert_allclose(s_str[:, 1], s_reg[:, 1], rtol=2 ** -23, atol=0)
+    np.testing.assert_allclose(out["streaming"][1], out["registers"][1], rtol=1e-6)
+    grads = []
+    for ptr in (dl.ptr, shifted):
+        g = C.Buffer((rows, classes))
+        C.check(C.lib().vc_hip_xent_backward_value(ptr, dt.ptr, out["registers"][0].ptr, ctypes.c_float(1.0), rows,
+                                                   classes, g.ptr))
+        grads.append(g.numpy())
+    np.testing.assert_array_equal(grads[1], grads[0])
 
 
 def _special_rows(classes, rng):

@@ -27,6 +27,28 @@ def device(request):
     return request.param
 
 
+GEMM_DEVICES = DEVICES + [pytest.param("hip-simple", id="hip-simple", marks=pytest.mark.gpu)]
+
+
+@pytest.fixture(params=GEMM_DEVICES)
+def gemm_device(request):
+    """A device for matmul, gradcheck and MLP tests: cpu, hip with the MFMA
+    GEMM, and hip with the portable FMA GEMM selected (the reference re-runs
+    these tests with its portable kernel forced,
+    tests/python/test_performance_paths.py:89-103)."""
+    if request.param == "cpu":
+        yield "cpu"
+        return
+    assert vc.hip_available(), "the hip device must be available on a GPU run"
+    kernel = "simple" if request.param == "hip-simple" else "mfma"
+    previous = vc.hip_set_gemm_kernel(kernel)
+    try:
+        assert vc.hip_gemm_kernel() == kernel
+        yield "hip"
+    finally:
+        vc.hip_set_gemm_kernel(previous)
+
+
 def npy(t):
     return t.to("cpu").numpy()
 
@@ -99,15 +121,15 @@ def test_broadcasting(device):
         m + T(np.ones((2, 2)), device)
 
 
-def test_matmul_transpose_and_batches(device):
-    a, b = T([[1, 2, 3], [4, 5, 6]], device), T([[7, 8], [9, 10], [11, 12]], device)
+def test_matmul_transpose_and_batches(gemm_device):
+    a, b = T([[1, 2, 3], [4, 5, 6]], gemm_device), T([[7, 8], [9, 10], [11, 12]], gemm_device)
     close(a @ b, [58, 64, 139, 154])
     close(a.transpose(), [1, 4, 2, 5, 3, 6])
-    close(T(np.arange(1, 9).reshape(2, 2, 2), device).transpose(), [1, 3, 2, 4, 5, 7, 6, 8])
+    close(T(np.arange(1, 9).reshape(2, 2, 2), gemm_device).transpose(), [1, 3, 2, 4, 5, 7, 6, 8])
     with pytest.raises(ValueError):
-        a @ T(np.ones((4, 2)), device)
+        a @ T(np.ones((4, 2)), gemm_device)
     with pytest.raises(ValueError):
-        T(np.ones((2, 2, 3)), device) @ T(np.ones((3, 3, 1)), device)
+        T(np.ones((2, 2, 3)), gemm_device) @ T(np.ones((3, 3, 1)), gemm_device)
 
 
 def test_reductions_activations_and_softmax(device):
@@ -165,21 +187,21 @@ def test_softmax_stable_for_huge_logits(device):
 # --- autograd semantics ------------------------------------------------------------
 
 
-def test_autograd_known_answers(device):
-    x = T([1, 2, 3], device, True)
+def test_autograd_known_answers(gemm_device):
+    x = T([1, 2, 3], gemm_device, True)
     ((x * x) + x).sum().backward()
     close(x.grad, [3, 5, 7])
     x.zero_grad()
     assert x.grad is None
-    x, b = T([[1, 2, 3], [4, 5, 6]], device, True), T([0.1, 0.2, 0.3], device, True)
+    x, b = T([[1, 2, 3], [4, 5, 6]], gemm_device, True), T([0.1, 0.2, 0.3], gemm_device, True)
     (x + b).sum().backward()
     close(x.grad, np.ones(6))
     close(b.grad, [2, 2, 2])
-    a, w = T([[1, 2, 3], [4, 5, 6]], device, True), T([[1, 2], [3, 4], [5, 6]], device, True)
+    a, w = T([[1, 2, 3], [4, 5, 6]], gemm_device, True), T([[1, 2], [3, 4], [5, 6]], gemm_device, True)
     a.matmul(w).sum().backward()
     close(a.grad, [3, 7, 11, 3, 7, 11])
     close(w.grad, [5, 5, 7, 7, 9, 9])
-    gx, gb = T([[-1, 2, 3], [-4, 5, 6]], device, True), T([0.5, 1.0, -2.0], device, True)
+    gx, gb = T([[-1, 2, 3], [-4, 5, 6]], gemm_device, True), T([0.5, 1.0, -2.0], gemm_device, True)
     (gx + gb).relu().sum().backward()
     close(gx.grad, [0, 1, 1, 0, 1, 1])
     close(gb.grad, [0, 2, 2])
@@ -202,8 +224,8 @@ def test_gradient_accumulation_and_retain_grad(device):
         T([1.0], device).retain_grad()
 
 
-def test_batched_and_broadcast_matmul_grads(device):
-    a, w = T([[[1, 2]], [[3, 4]]], device, True), T([[1, 0], [0, 2]], device, True)
+def test_batched_and_broadcast_matmul_grads(gemm_device):
+    a, w = T([[[1, 2]], [[3, 4]]], gemm_device, True), T([[1, 0], [0, 2]], gemm_device, True)
     y = a.matmul(w)
     assert y.shape == [2, 1, 2]
     close(y, [1, 4, 3, 8])
@@ -328,9 +350,9 @@ def _relu_net(device, retain=False, reuse=False, seed=7):
     return h, [w1, b1, w2]
 
 
-def test_relu_fold_gives_the_unfolded_bits(device):
-    _, folded = _relu_net(device)
-    h, plain = _relu_net(device, retain=True)  # a kept gradient turns the fold off
+def test_relu_fold_gives_the_unfolded_bits(gemm_device):
+    _, folded = _relu_net(gemm_device)
+    h, plain = _relu_net(gemm_device, retain=True)  # a kept gradient turns the fold off
     for p, q in zip(folded, plain):
         np.testing.assert_array_equal(npy(p.grad), npy(q.grad))
     _, cpu = _relu_net("cpu")
@@ -486,6 +508,29 @@ def test_partial_in_place_update_of_a_deferred_operand():
 
 
 @hip_only
+def test_sgd_with_a_gradient_aliasing_its_parameter_and_a_pending_product():
+    # w.backward(w) stores w itself as w.grad (the same storage). A product
+    # recorded on w is still pending when sgd_step runs, so the update moves
+    # w to a fresh buffer; it must read the gradient from w's current
+    # contents, giving w - lr * w as the reference's host loop does.
+    rng = np.random.default_rng(21)
+    xs, w0 = rng.standard_normal((33, 20)).astype(np.float32), rng.standard_normal((20, 18)).astype(np.float32)
+
+    def run():
+        x = vc.Tensor(xs, device="hip")
+        w = vc.Tensor(w0, requires_grad=True, device="hip")
+        p = x @ w
+        w.backward(w)
+        vc.sgd_step([w], 0.25)
+        return [npy(p), npy(w)]
+
+    eager, deferred = _eager_then_deferred(run)
+    _assert_same_bits(eager, deferred)
+    np.testing.assert_array_equal(deferred[1], w0 - np.float32(0.25) * w0)
+    np.testing.assert_allclose(deferred[0], xs.astype(np.float64) @ w0, rtol=1e-4, atol=1e-4 * np.sqrt(20))
+
+
+@hip_only
 def test_long_chain_of_deferred_products():
     # 3000 products, each of the one before, none read until the end: the
     # chain is computed in bounded pieces and gives the eager bits.
@@ -598,17 +643,17 @@ GRADCHECK = [
 
 
 @pytest.mark.parametrize("name,fn,factories", GRADCHECK, ids=[c[0] for c in GRADCHECK])
-def test_gradcheck(device, name, fn, factories, eps=5e-3):
+def test_gradcheck(gemm_device, name, fn, factories, eps=5e-3):
     rng = np.random.default_rng(zlib.crc32(name.encode()))
     inputs = [f(rng) for f in factories]
-    leaves = [vc.Tensor(x, requires_grad=True, device=device) for x in inputs]
+    leaves = [vc.Tensor(x, requires_grad=True, device=gemm_device) for x in inputs]
     out = fn(*leaves)
     weights = np.random.default_rng(99).uniform(0.5, 1.5, size=out.shape).astype(np.float32)
-    (out * vc.Tensor(weights, device=device)).sum().backward()
+    (out * vc.Tensor(weights, device=gemm_device)).sum().backward()
 
     def objective(values):
-        r = fn(*[vc.Tensor(v, device=device) for v in values])
-        return float((r * vc.Tensor(weights, device=device)).sum().item())
+        r = fn(*[vc.Tensor(v, device=gemm_device) for v in values])
+        return float((r * vc.Tensor(weights, device=gemm_device)).sum().item())
 
     for i, (leaf, base) in enumerate(zip(leaves, inputs)):
         assert leaf.grad is not None, f"input {i} received no gradient"
@@ -620,7 +665,7 @@ def test_gradcheck(device, name, fn, factories, eps=5e-3):
             minus[i].reshape(-1)[p] -= eps
             numeric[p] = (objective(plus) - objective(minus)) / (2 * eps)
         np.testing.assert_allclose(npy(leaf.grad).reshape(-1), numeric, rtol=1e-2, atol=1e-2,
-                                   err_msg=f"input {i} of {name} on {device}")
+                                   err_msg=f"input {i} of {name} on {gemm_device}")
 
 
 # --- kernels at edge shapes (test_performance_paths.py) ----------------------------------
@@ -631,22 +676,22 @@ GEMM_SHAPES = [(3, 5, 7), (4, 33, 33), (8, 256, 12), (16, 512, 24), (9, 257, 13)
 
 
 @pytest.mark.parametrize("m,k,n", GEMM_SHAPES)
-def test_matmul_edge_shapes(device, m, k, n):
+def test_matmul_edge_shapes(gemm_device, m, k, n):
     rng = np.random.default_rng(m * 10007 + k * 101 + n)
     a = rng.uniform(-1, 1, size=(m, k)).astype(np.float32)
     b = rng.uniform(-1, 1, size=(k, n)).astype(np.float32)
-    got = npy(vc.Tensor(a, device=device) @ vc.Tensor(b, device=device))
+    got = npy(vc.Tensor(a, device=gemm_device) @ vc.Tensor(b, device=gemm_device))
     np.testing.assert_allclose(got, a.astype(np.float64) @ b.astype(np.float64), rtol=1e-4, atol=1e-4 * np.sqrt(k))
 
 
 @pytest.mark.parametrize("m,k,n", [(128, 64, 192), (64, 128, 64), (100, 72, 90), (128, 60, 128)])
-def test_matmul_gradients_transposed_in_place(device, m, k, n):
+def test_matmul_gradients_transposed_in_place(gemm_device, m, k, n):
     rng = np.random.default_rng(m + k + n)
     a = rng.uniform(-1, 1, size=(m, k)).astype(np.float32)
     b = rng.uniform(-1, 1, size=(k, n)).astype(np.float32)
     g = rng.uniform(-1, 1, size=(m, n)).astype(np.float32)
-    ta, tb = vc.Tensor(a, requires_grad=True, device=device), vc.Tensor(b, requires_grad=True, device=device)
-    (ta @ tb).backward(vc.Tensor(g, device=device))
+    ta, tb = vc.Tensor(a, requires_grad=True, device=gemm_device), vc.Tensor(b, requires_grad=True, device=gemm_device)
+    (ta @ tb).backward(vc.Tensor(g, device=gemm_device))
     np.testing.assert_allclose(npy(ta.grad), g.astype(np.float64) @ b.T, rtol=1e-4, atol=1e-4 * np.sqrt(n))
     np.testing.assert_allclose(npy(tb.grad), a.T.astype(np.float64) @ g, rtol=1e-4, atol=1e-4 * np.sqrt(m))
 
@@ -706,7 +751,7 @@ def test_broadcast_gradient_reduction_shapes(device):
         np.testing.assert_allclose(npy(b.grad), expected, rtol=1e-4, atol=1e-4)
 
 
-def test_mlp_learns_nonlinear_spiral(device):
+def test_mlp_learns_nonlinear_spiral(gemm_device):
     rng = np.random.default_rng(0)
     feats, labels = [], []
     for k in range(3):
@@ -714,9 +759,9 @@ def test_mlp_learns_nonlinear_spiral(device):
         t = np.linspace(4.0 * k, 4.0 * (k + 1), 60) + rng.normal(scale=0.2, size=60)
         feats.append(np.column_stack([r * np.sin(t), r * np.cos(t)]))
         labels += [k] * 60
-    x = vc.Tensor(np.concatenate(feats).astype(np.float32), device=device)
+    x = vc.Tensor(np.concatenate(feats).astype(np.float32), device=gemm_device)
     first, second = vc.Linear(2, 64, 1), vc.Linear(64, 3, 2)
-    params = [p.to(device).detach() for p in (first.weight, first.bias, second.weight, second.bias)]
+    params = [p.to(gemm_device).detach() for p in (first.weight, first.bias, second.weight, second.bias)]
     for p in params:
         p.requires_grad = True
     first.weight, first.bias, second.weight, second.bias = params
@@ -839,6 +884,15 @@ def test_hip_loss_item_is_published_without_a_full_synchronisation():
 def test_hip_gemm_kernel_reported():
     assert vc.hip_gemm_kernel() in ("mfma", "simple")
     assert "gfx950" in vc.hip_device_name()
+    previous = vc.hip_set_gemm_kernel("simple")
+    try:
+        assert vc.hip_gemm_kernel() == "simple"
+        with pytest.raises(ValueError, match="unknown GEMM kernel"):
+            vc.hip_set_gemm_kernel("tiled")
+        assert vc.hip_gemm_kernel() == "simple"
+    finally:
+        vc.hip_set_gemm_kernel(previous)
+    assert vc.hip_gemm_kernel() == previous
 
 
 def test_hip_unavailable_is_loud_on_cpu_hosts():
@@ -848,6 +902,9 @@ def test_hip_unavailable_is_loud_on_cpu_hosts():
         vc.Tensor([1.0], device="hip")
     with pytest.raises(RuntimeError):
         vc.Tensor([1.0], device="metal")
+    with pytest.raises(RuntimeError, match="HIP"):
+        vc.hip_set_gemm_kernel("simple")
+    assert vc.hip_gemm_kernel() == "unavailable"
 
 
 @pytest.mark.parametrize("call", [

@@ -23,6 +23,18 @@ def hip_device():
     assert vc.hip_available(), "the hip device must be available on a GPU run"
 
 
+@pytest.fixture(params=["mfma", "simple"])
+def gemm_kernel(request):
+    """The MLP tests run on the MFMA GEMM and again with the portable FMA GEMM
+    selected (tests/python/test_performance_paths.py:89-103 re-runs the
+    reference's MLP tests with its portable kernel forced)."""
+    previous = vc.hip_set_gemm_kernel(request.param)
+    try:
+        yield request.param
+    finally:
+        vc.hip_set_gemm_kernel(previous)
+
+
 def H(x, grad=False):
     return vc.Tensor(np.asarray(x, dtype=np.float32), requires_grad=grad, device="hip")
 
@@ -47,7 +59,7 @@ def mlp_logits(params, x):
 # --- spiral classifier step (2 -> 64 -> 3, 300 points, lr 1.0) -------------------------
 
 
-def test_spiral_steps_match_reference_fixture(golden):
+def test_spiral_steps_match_reference_fixture(golden, gemm_kernel):
     sp = W.spiral()
     params = build_mlp(sp["weights"], sp["biases"])
     x = H(sp["x"])
@@ -195,7 +207,7 @@ def test_cross_entropy_matches_reference_fixture(golden):
 # --- MLP train step (8192 x 1024 -> 4096 -> 4096 -> 1000) ----------------------------
 
 
-def test_mlp_small_matches_reference_fixture(golden):
+def test_mlp_small_matches_reference_fixture(golden, gemm_kernel):
     n = 3
     params = build_mlp([golden[f"mlp_w{i}"] for i in range(n)], [golden[f"mlp_b{i}"] for i in range(n)])
     x, t = H(golden["mlp_x"]), golden["mlp_targets"]
@@ -218,7 +230,7 @@ def test_mlp_small_matches_reference_fixture(golden):
         np.testing.assert_allclose(params[2 * i].numpy(), golden[f"mlp_w{i}_after3"], rtol=1e-5, atol=1e-7)
 
 
-def test_mlp_workload_architecture_against_oracle():
+def test_mlp_workload_architecture_against_oracle(gemm_kernel):
     """The full 1024 -> 4096 -> 4096 -> 1000 network on a 64-row batch."""
     m = W.mlp(batch=64)
     params = build_mlp(m["weights"], m["biases"])

@@ -15,6 +15,7 @@ from ._vectorcore import (  # noqa: F401
     hip_defer_products,
     hip_device_name,
     hip_gemm_kernel,
+    hip_set_gemm_kernel,
     hip_pool_stats,
     hip_profile,
     hip_profile_read,

@@ -7,6 +7,7 @@ library has not been built.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from pathlib import Path
 
@@ -31,6 +32,7 @@ _SIGNATURES = {
     "vc_hip_device_name": ([], ctypes.c_char_p),
     "vc_hip_last_error": ([], ctypes.c_char_p),
     "vc_hip_gemm_kernel": ([], ctypes.c_char_p),
+    "vc_hip_set_gemm_kernel": ([ctypes.c_char_p], _i),
     "vc_hip_alloc": ([_sz, ctypes.POINTER(_vp)], _i),
     "vc_hip_release": ([_vp], _i),
     "vc_hip_upload": ([_vp, _vp, _sz], _i),
@@ -188,3 +190,14 @@ def profile_read() -> dict:
             out[label.value.decode()] = dict(launches=launches.value, ms=ms.value, flops=flops.value,
                                              bytes=nbytes.value)
     return out
+
+
+@contextlib.contextmanager
+def gemm_kernel(name: str):
+    """Run the enclosed calls with GEMM kernel `name` ("mfma" or "simple"), then restore the previous one."""
+    previous = lib().vc_hip_gemm_kernel().decode()
+    check(lib().vc_hip_set_gemm_kernel(name.encode()))
+    try:
+        yield name
+    finally:
+        check(lib().vc_hip_set_gemm_kernel(previous.encode()))

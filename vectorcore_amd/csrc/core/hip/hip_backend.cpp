@@ -243,6 +243,10 @@ bool HipBackend::available() const noexcept { return vc_hip_available() != 0; }
 std::string HipBackend::device_name() const { return vc_hip_device_name(); }
 std::string HipBackend::last_error() const { return vc_hip_last_error(); }
 std::string HipBackend::gemm_kernel() const { return vc_hip_gemm_kernel(); }
+void HipBackend::set_gemm_kernel(const std::string& name) {
+    require(*this);
+    check(vc_hip_set_gemm_kernel(name.c_str()), "HIP GEMM kernel selection failed");
+}
 
 std::shared_ptr<Storage> HipBackend::allocate(std::size_t elements) {
     require(*this);
@@ -446,7 +450,12 @@ void HipBackend::axpy_batch(const std::vector<AxpyItem>& items, float alpha) {
         if (it.count == 0) continue;
         outputs.push_back(t.ptr() + it.target_offset);
         targets.push_back(current.back()->ptr() + it.target_offset);
-        sources.push_back(dptr(*it.source, it.source_offset));
+        // A source in the target's own storage (a gradient that aliases its
+        // parameter, e.g. from w.backward(w)) is read from the buffer holding
+        // the current contents: before_write may have given the target a
+        // fresh, unwritten buffer.
+        sources.push_back(it.source == it.target ? current.back()->ptr() + it.source_offset
+                                                 : dptr(*it.source, it.source_offset));
         counts.push_back(it.count);
     }
     if (outputs.empty()) return;

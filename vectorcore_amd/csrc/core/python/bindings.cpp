@@ -191,6 +191,17 @@ PYBIND11_MODULE(_vectorcore, m) {
     m.def("hip_device_name", &hip_device_name);
     m.def("hip_gemm_kernel", [] { return HipBackend::instance().gemm_kernel(); },
           "Which HIP matmul kernel is active: 'mfma', 'simple' or 'unavailable'.");
+    m.def(
+        "hip_set_gemm_kernel",
+        [](const std::string& name) {
+            auto& b = HipBackend::instance();
+            const std::string previous = b.gemm_kernel();
+            b.set_gemm_kernel(name);
+            return previous;
+        },
+        py::arg("name"),
+        "Select the HIP matmul kernel for later products ('mfma' or 'simple', the portable FMA kernel); "
+        "returns the previous one.");
     m.def("synchronize", &vectorcore::synchronize,
           "Wait for all queued device work; reading tensor values does this automatically.");
 

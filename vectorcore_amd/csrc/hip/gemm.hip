@@ -473,7 +473,8 @@ __global__ __launch_bounds__(256) void transpose64_kernel(const float* __restric
     }
 }
 
-// Portable LDS-tiled FMA kernel (VECTORCORE_HIP_GEMM=simple): 16 x 16 outputs
+// Portable LDS-tiled FMA kernel (VECTORCORE_HIP_GEMM=simple or
+// vc_hip_set_gemm_kernel("simple"), and tiny products): 16 x 16 outputs
 // per 256-thread workgroup, one per thread.
 template <bool TA, bool TB>
 __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
@@ -532,12 +533,13 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     if (M < 0 || N < 0 || K < 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "negative matrix dimension");
     if (M == 0 || N == 0 || batch == 0) return;
     if (!a || !b || !c) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul: null buffer");
+    const bool force_simple = d.simple_gemm.load();  // the kernel in force for this call
     // A single large NN product runs as NT on a transposed copy of B: the
     // kernel is ~3.5% faster when both operands are contiguous along k, which
     // outweighs the copy (2 K N floats of traffic) once M >= 4096. The LDS
     // tiles, and so the bits, are those of the NN kernel. (K is bounded by the
     // transpose's grid: 65535 tiles of 64 rows.)
-    if (!ta && !tb && batch == 1 && reduce == 1 && !d.simple_gemm && M >= kNnViaNtMinRows && N % 4 == 0 &&
+    if (!ta && !tb && batch == 1 && reduce == 1 && !force_simple && M >= kNnViaNtMinRows && N % 4 == 0 &&
         K % 4 == 0 && K <= int64_t(65535) * 64 && aligned16(a) && aligned16(b) && !relu_mask) {
         Profiled prof("gemm_nn", 2.0 * double(M) * double(N) * double(K),
                       4.0 * double(M * K + 2 * K * N + M * N) + (bias ? 4.0 * double(N) : 0.0));
@@ -556,7 +558,7 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     // 128 x 128 MFMA tile there is mostly padding, and its fixed latency
     // (~8 us) is several times the FMA kernel's whole run.
     const bool simple =
-        d.simple_gemm || (double(M) * double(N) * double(K) * double(batch) * double(reduce) <= kTinyMacs && K <= 128);
+        force_simple || (double(M) * double(N) * double(K) * double(batch) * double(reduce) <= kTinyMacs && K <= 128);
     const int64_t tiles = simple ? tiles_m_simple * tiles_n_simple : tiles_m * tiles_n;
     if (tiles > std::numeric_limits<int>::max() / 2) fail(VC_HIP_ERR_OVERFLOW, "matmul output has too many tiles");
     // Byte offsets relative to a tile origin are 32-bit: 128 rows of any

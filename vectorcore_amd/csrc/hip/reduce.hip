@@ -18,6 +18,8 @@
 
 #include <algorithm>
 #include <limits>
+#include <memory>
+#include <vector>
 
 namespace vchip {
 namespace {
@@ -316,31 +318,149 @@ void check_i32(int64_t v, const char* what) {
     if (v > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, std::string(what) + " exceeds the int32 index range");
 }
 
-void column_sum(Device& d, const float* in, float* out, int64_t outer, int64_t len, int64_t inner, const char* label) {
-    const bool vec = inner % 4 == 0 && aligned16(in);
-    const int64_t width = vec ? 4 * kColLanes : kColLanes;
-    const int64_t chunks = (inner + width - 1) / width;
-    const int64_t blocks_x = outer * chunks;
-    // Segments: a function of the shape only; aim at ~2048 workgroups, at
-    // least 64 rows per segment, at most 64 segments.
+// Segments of a column sum: a function of the shape only; aim at ~2048
+// workgroups, at least 64 rows per segment, at most 64 segments.
+struct ColumnPlan {
+    bool vec;
+    int64_t chunks, segs, seg_len;
+};
+
+ColumnPlan column_plan(const float* in, int64_t outer, int64_t len, int64_t inner) {
+    ColumnPlan c{};
+    c.vec = inner % 4 == 0 && aligned16(in);
+    const int64_t width = c.vec ? 4 * kColLanes : kColLanes;
+    c.chunks = (inner + width - 1) / width;
+    const int64_t blocks_x = outer * c.chunks;
+    if (blocks_x > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, "reduction too large");
     int64_t segs = std::max<int64_t>(1, (2048 + blocks_x - 1) / blocks_x);
     segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / 64), int64_t(kMaxColSegs)});
-    const int64_t seg_len = (len + segs - 1) / segs;
-    segs = (len + seg_len - 1) / seg_len;
-    if (blocks_x > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, "reduction too large");
+    c.seg_len = (len + segs - 1) / segs;
+    c.segs = (len + c.seg_len - 1) / c.seg_len;
+    return c;
+}
+
+void column_sum(Device& d, const ColumnPlan& c, const float* in, float* out, double* part, int64_t outer,
+                int64_t len, int64_t inner, const char* label) {
     const int64_t total = outer * inner;
-    Scratch part(size_t(segs * total) * sizeof(double));
-    const dim3 grid(static_cast<unsigned>(blocks_x), static_cast<unsigned>(segs));
-    if (vec)
-        launch(colsum_tile_kernel<true>, grid, dim3(kBlock), 0, d.stream, in, part.as<double>(), outer, len,
-                           inner, seg_len, chunks);
+    const dim3 grid(static_cast<unsigned>(outer * c.chunks), static_cast<unsigned>(c.segs));
+    if (c.vec)
+        launch(colsum_tile_kernel<true>, grid, dim3(kBlock), 0, d.stream, in, part, outer, len, inner, c.seg_len,
+               c.chunks);
     else
-        launch(colsum_tile_kernel<false>, grid, dim3(kBlock), 0, d.stream, in, part.as<double>(), outer, len,
-                           inner, seg_len, chunks);
+        launch(colsum_tile_kernel<false>, grid, dim3(kBlock), 0, d.stream, in, part, outer, len, inner, c.seg_len,
+               c.chunks);
     after_launch(label);
-    launch(colsum_combine_kernel, dim3(unsigned((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, d.stream,
-                       part.as<double>(), out, total, int(segs));
+    launch(colsum_combine_kernel, dim3(unsigned((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, d.stream, part, out,
+           total, int(c.segs));
     after_launch(label);
+}
+
+// Segments of a max/argmax over a long axis with few outputs (>= 16 rows each).
+struct BestPlan {
+    int64_t segs, seg_len;
+};
+
+BestPlan best_plan(int64_t len, int64_t total, int64_t target_threads) {
+    BestPlan b{};
+    int64_t segs = std::min<int64_t>((target_threads + total - 1) / total, (len + 15) / 16);
+    segs = std::max<int64_t>(1, std::min<int64_t>(segs, 1024));
+    b.seg_len = (len + segs - 1) / segs;
+    b.segs = (len + b.seg_len - 1) / b.seg_len;
+    return b;
+}
+
+// Device memory for one call's partial results: pool buffers
+// (vc_hip_reduce_axis) or the static array (vc_hip_reduce_axis_noalloc).
+class PartialMemory {
+public:
+    virtual ~PartialMemory() = default;
+    virtual void* take(size_t bytes) = 0;
+};
+
+class PoolPartials final : public PartialMemory {
+public:
+    void* take(size_t bytes) override {
+        held_.push_back(std::make_unique<Scratch>(bytes));
+        return held_.back()->as<void>();
+    }
+
+private:
+    std::vector<std::unique_ptr<Scratch>> held_;
+};
+
+void reduce_axis(const float* in, float* out, int64_t outer, int64_t len, int64_t inner, int op,
+                 PartialMemory& memory) {
+    Device& d = require_device();
+    if (op < VC_REDUCE_SUM || op > VC_REDUCE_ARGMAX) fail(VC_HIP_ERR_INVALID_ARGUMENT, "unknown reduction");
+    if (len == 0 && op != VC_REDUCE_SUM) fail(VC_HIP_ERR_INVALID_ARGUMENT, "max/argmax over an empty axis is undefined");
+    const int64_t total = outer * inner;
+    if (total == 0) return;
+    const char* label = op == VC_REDUCE_SUM ? "reduce_axis_sum" : op == VC_REDUCE_MAX ? "reduce_axis_max" : "reduce_axis_argmax";
+    if (len == 0) {  // sum over an empty axis is zero
+        launch(zero_kernel, dim3(grid_1d(size_t(total), kBlock, 1024)), dim3(kBlock), 0, d.stream, out, total);
+        after_launch(label);
+        return;
+    }
+    check_i32(len, "reduction axis length");
+    Profiled p(label, double(outer * len * inner), 4.0 * double(outer * len * inner + total));
+    const int64_t target_threads = int64_t(d.cu_count) * 1024;
+    if (inner == 1) {
+        // One wavefront per row; rows of < 64 elements leave lanes idle but stay correct.
+        const bool vec = len % 4 == 0 && aligned16(in);
+        const unsigned grid = unsigned(std::min<int64_t>((outer + 3) / 4, int64_t(d.cu_count) * 64));
+        const int64_t nv = vec ? (len + kWave * 4 - 1) / (kWave * 4) : 0;
+#define VC_ROWS_NV(OP, VEC, NV) \
+    launch((rows_kernel<OP, VEC, NV>), dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len)
+#define VC_ROWS(OP)                                 \
+    if (!vec) VC_ROWS_NV(OP, false, 0);             \
+    else if (nv <= 1) VC_ROWS_NV(OP, true, 1);      \
+    else if (nv <= 2) VC_ROWS_NV(OP, true, 2);      \
+    else if (nv <= 4) VC_ROWS_NV(OP, true, 4);      \
+    else if (nv <= 8) VC_ROWS_NV(OP, true, 8);      \
+    else if (nv <= 16) VC_ROWS_NV(OP, true, 16);    \
+    else VC_ROWS_NV(OP, true, 0)
+        if (op == VC_REDUCE_SUM) { VC_ROWS(0); }
+        else if (op == VC_REDUCE_MAX) { VC_ROWS(1); }
+        else { VC_ROWS(2); }
+#undef VC_ROWS
+#undef VC_ROWS_NV
+        after_launch(label);
+        p.done();
+        return;
+    }
+    if (total >= target_threads || len < 64) {
+        const unsigned grid = grid_1d(size_t(total), kBlock, unsigned(d.cu_count) * 64);
+        if (op == VC_REDUCE_SUM) launch(cols_kernel<0>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
+        else if (op == VC_REDUCE_MAX) launch(cols_kernel<1>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
+        else launch(cols_kernel<2>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
+        after_launch(label);
+        p.done();
+        return;
+    }
+    if (op == VC_REDUCE_SUM) {
+        const ColumnPlan c = column_plan(in, outer, len, inner);
+        double* part = static_cast<double*>(memory.take(size_t(c.segs * total) * sizeof(double)));
+        column_sum(d, c, in, out, part, outer, len, inner, label);
+        p.done();
+        return;
+    }
+    // max/argmax with few outputs: split the axis into segments.
+    const BestPlan b = best_plan(len, total, target_threads);
+    const dim3 grid1(unsigned((total + kBlock - 1) / kBlock), unsigned(b.segs));
+    const unsigned grid2 = unsigned((total + kBlock - 1) / kBlock);
+    char* mem = static_cast<char*>(memory.take(size_t(b.segs * total) * (sizeof(float) + sizeof(int))));
+    float* pv = reinterpret_cast<float*>(mem);
+    int* pi = reinterpret_cast<int*>(mem + size_t(b.segs * total) * sizeof(float));
+    launch(cols_best_partial_kernel, grid1, dim3(kBlock), 0, d.stream, in, pv, pi, outer, len, inner, b.seg_len);
+    after_launch(label);
+    if (op == VC_REDUCE_MAX)
+        launch(cols_best_combine_kernel<1>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv, pi, out, outer, len, inner,
+               b.segs);
+    else
+        launch(cols_best_combine_kernel<2>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv, pi, out, outer, len, inner,
+               b.segs);
+    after_launch(label);
+    p.done();
 }
 
 }  // namespace
@@ -375,81 +495,10 @@ int vc_hip_reduce_sum(const float* in, size_t count, float* out) {
     });
 }
 
-int vc_hip_reduce_axis(const float* in, float* out, size_t outer_, size_t length_, size_t inner_, int op) {
+int vc_hip_reduce_axis(const float* in, float* out, size_t outer, size_t length, size_t inner, int op) {
     return guard([&] {
-        Device& d = require_device();
-        if (op < VC_REDUCE_SUM || op > VC_REDUCE_ARGMAX) fail(VC_HIP_ERR_INVALID_ARGUMENT, "unknown reduction");
-        if (length_ == 0 && op != VC_REDUCE_SUM)
-            fail(VC_HIP_ERR_INVALID_ARGUMENT, "max/argmax over an empty axis is undefined");
-        const int64_t outer = int64_t(outer_), len = int64_t(length_), inner = int64_t(inner_);
-        const int64_t total = outer * inner;
-        if (total == 0) return;
-        const char* label = op == VC_REDUCE_SUM ? "reduce_axis_sum" : op == VC_REDUCE_MAX ? "reduce_axis_max" : "reduce_axis_argmax";
-        if (len == 0) {  // sum over an empty axis is zero
-            launch(zero_kernel, dim3(grid_1d(size_t(total), kBlock, 1024)), dim3(kBlock), 0, d.stream, out, total);
-            after_launch(label);
-            return;
-        }
-        check_i32(len, "reduction axis length");
-        Profiled p(label, double(outer * len * inner), 4.0 * double(outer * len * inner + total));
-        const int64_t target_threads = int64_t(d.cu_count) * 1024;
-        if (inner == 1) {
-            // One wavefront per row; rows of < 64 elements leave lanes idle but stay correct.
-            const bool vec = len % 4 == 0 && aligned16(in);
-            const unsigned grid = unsigned(std::min<int64_t>((outer + 3) / 4, int64_t(d.cu_count) * 64));
-            const int64_t nv = vec ? (len + kWave * 4 - 1) / (kWave * 4) : 0;
-#define VC_ROWS_NV(OP, VEC, NV) \
-    launch((rows_kernel<OP, VEC, NV>), dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len)
-#define VC_ROWS(OP)                                 \
-    if (!vec) VC_ROWS_NV(OP, false, 0);             \
-    else if (nv <= 1) VC_ROWS_NV(OP, true, 1);      \
-    else if (nv <= 2) VC_ROWS_NV(OP, true, 2);      \
-    else if (nv <= 4) VC_ROWS_NV(OP, true, 4);      \
-    else if (nv <= 8) VC_ROWS_NV(OP, true, 8);      \
-    else if (nv <= 16) VC_ROWS_NV(OP, true, 16);    \
-    else VC_ROWS_NV(OP, true, 0)
-            if (op == VC_REDUCE_SUM) { VC_ROWS(0); }
-            else if (op == VC_REDUCE_MAX) { VC_ROWS(1); }
-            else { VC_ROWS(2); }
-#undef VC_ROWS
-#undef VC_ROWS_NV
-            after_launch(label);
-            p.done();
-            return;
-        }
-        if (total >= target_threads || len < 64) {
-            const unsigned grid = grid_1d(size_t(total), kBlock, unsigned(d.cu_count) * 64);
-            if (op == VC_REDUCE_SUM) launch(cols_kernel<0>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
-            else if (op == VC_REDUCE_MAX) launch(cols_kernel<1>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
-            else launch(cols_kernel<2>, dim3(grid), dim3(kBlock), 0, d.stream, in, out, outer, len, inner);
-            after_launch(label);
-            p.done();
-            return;
-        }
-        if (op == VC_REDUCE_SUM) {
-            column_sum(d, in, out, outer, len, inner, label);
-            p.done();
-            return;
-        }
-        // max/argmax with few outputs: split the axis into segments of >= 16 rows.
-        int64_t segs = std::min<int64_t>((target_threads + total - 1) / total, (len + 15) / 16);
-        segs = std::max<int64_t>(1, std::min<int64_t>(segs, 1024));
-        const int64_t seg_len = (len + segs - 1) / segs;
-        segs = (len + seg_len - 1) / seg_len;
-        const dim3 grid1(unsigned((total + kBlock - 1) / kBlock), unsigned(segs));
-        const unsigned grid2 = unsigned((total + kBlock - 1) / kBlock);
-        Scratch pv(size_t(segs * total) * sizeof(float)), pi(size_t(segs * total) * sizeof(int));
-        launch(cols_best_partial_kernel, grid1, dim3(kBlock), 0, d.stream, in, pv.as<float>(), pi.as<int>(), outer,
-                           len, inner, seg_len);
-        after_launch(label);
-        if (op == VC_REDUCE_MAX)
-            launch(cols_best_combine_kernel<1>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv.as<float>(),
-                               pi.as<int>(), out, outer, len, inner, segs);
-        else
-            launch(cols_best_combine_kernel<2>, dim3(grid2), dim3(kBlock), 0, d.stream, in, pv.as<float>(),
-                               pi.as<int>(), out, outer, len, inner, segs);
-        after_launch(label);
-        p.done();
+        PoolPartials memory;
+        reduce_axis(in, out, int64_t(outer), int64_t(length), int64_t(inner), op, memory);
     });
 }
 

@@ -511,6 +511,16 @@ const char* vc_hip_gemm_kernel(void) {
     return d.simple_gemm ? "simple" : "mfma";
 }
 
+int vc_hip_set_gemm_kernel(const char* name) {
+    return guard([&] {
+        Device& d = require_device();
+        if (name && std::strcmp(name, "mfma") == 0) d.simple_gemm = false;
+        else if (name && std::strcmp(name, "simple") == 0) d.simple_gemm = true;
+        else fail(VC_HIP_ERR_INVALID_ARGUMENT, std::string("unknown GEMM kernel '") + (name ? name : "(null)") +
+                                                   "': expected \"mfma\" or \"simple\"");
+    });
+}
+
 int vc_hip_alloc(size_t bytes, void** out) {
     return guard([&] {
         if (!out) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_alloc: null output pointer");
@@ -561,6 +571,10 @@ int vc_hip_mirror_read(vc_hip_mirror* mirror, float* value) {
     return guard([&] {
         if (!mirror || !value) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_mirror_read: null pointer");
         check_hip(hipEventSynchronize(mirror->done), "HIP command failed");
+        // Report an error the stream has already recorded (work enqueued
+        // before this point that failed), without waiting for the rest.
+        const hipError_t state = hipStreamQuery(device().stream);
+        if (state != hipSuccess && state != hipErrorNotReady) check_hip(state, "HIP command failed");
         *value = *static_cast<volatile float*>(mirror->host);
     });
 }

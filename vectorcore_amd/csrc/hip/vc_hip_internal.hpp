@@ -6,6 +6,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <mutex>
@@ -67,7 +68,7 @@ struct Device {
     int cu_count = 0;
     hipStream_t stream = nullptr;
     bool sync_each_launch = false;  // VECTORCORE_HIP_SYNC_EACH=1 (fault localisation)
-    bool simple_gemm = false;       // VECTORCORE_HIP_GEMM=simple
+    std::atomic<bool> simple_gemm{false};  // VECTORCORE_HIP_GEMM=simple or vc_hip_set_gemm_kernel
 };
 
 // Initialises once (thread-safe) and makes the device current on this thread.

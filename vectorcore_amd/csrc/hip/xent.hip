@@ -8,9 +8,12 @@
 // backward evaluates, per element,
 //   dx_ij = ((c / s_i) * exp(x_ij - m_i)) + (j == t_i ? -c : -0.0)
 // (div -> negate -> sum -> mul -> sub/log/sum/exp rules of src/ops.cpp). These
-// kernels compute exactly those fp32 operations, in that order, reading the
-// logits once per pass: one wavefront per row, lanes striding the classes,
-// row statistics combined with cross-lane shuffles.
+// kernels compute those fp32 operations in that order, reading the logits
+// once per pass: one wavefront per row, lanes striding the classes, row
+// statistics combined with cross-lane exchanges. The one operation that is
+// not the reference's is exp (row_exp below: the hardware exp2, where the
+// reference calls the C library's expf), within ~1e-6 relative of it on the
+// terms that carry a row's sum.
 //
 // The reference's masked sum also turns any non-finite non-target log-prob
 // into NaN (inf * 0); the forward reproduces that.
@@ -33,6 +36,15 @@ __device__ inline f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p
 
 using red::Best;
 using red::kNone;
+
+// exp of a shifted logit s = x - m (s <= 0 unless the row holds NaN or
+// +inf): the hardware exp2 (V_EXP_F32, 1 ulp) of s * log2(e). Rounding the
+// product adds up to |s| 2^-24 relative error: at most ~1e-6 on the terms that
+// carry a row's sum (s > -16), ~5e-6 just above the underflow at s = -87.3,
+// below which the result is 0. Every kernel here takes its exponentials from
+// this one function, so a row's statistics and gradient have the same bits
+// whichever path (register-held or streaming) it takes.
+__device__ inline float row_exp(float s) { return __expf(s); }
 
 __device__ inline float row_max(const float* row, int64_t len, int lane, bool vec) {
     Best b = red::no_best();
@@ -131,9 +143,6 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
     } else {
         m = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, mx)));
     }
-    // exp via the hardware exp2 (V_EXP_F32, 1 ulp) of s * log2(e): the
-    // rounding of the product adds |s| 2^-24 relative error, at most ~2e-7 on
-    // the terms within e^-3 of the row maximum, which carry the sum (s <= 0).
     // Elements past the row give exp(-inf - m) = 0 (or NaN when m is -inf or
     // NaN, and then every real element's term is NaN too): adding them leaves
     // the sum unchanged.
@@ -143,10 +152,10 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
     for (int u = 0; u < NV; ++u) {
         const int a = lane * 4 + u * kWave * 4;
         const float s0 = v[u].x - m, s1 = v[u].y - m, s2 = v[u].z - m, s3 = v[u].w - m;
-        acc += double(__expf(s0));
-        acc += double(__expf(s1));
-        acc += double(__expf(s2));
-        acc += double(__expf(s3));
+        acc += double(row_exp(s0));
+        acc += double(row_exp(s1));
+        acc += double(row_exp(s2));
+        acc += double(row_exp(s3));
         nonfinite |= (a < len) & (!isfinite(s0) | !isfinite(s1) | !isfinite(s2) | !isfinite(s3));
     }
     int bad = 0;  // a non-target log-prob that is not finite
@@ -247,17 +256,17 @@ __global__ __launch_bounds__(kBlock) void xent_rows_kernel(const float* __restri
         for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
             const f4 v = ld4(row + a);
             const float s0 = v.x - m, s1 = v.y - m, s2 = v.z - m, s3 = v.w - m;
-            acc += double(expf(s0));
-            acc += double(expf(s1));
-            acc += double(expf(s2));
-            acc += double(expf(s3));
+            acc += double(row_exp(s0));
+            acc += double(row_exp(s1));
+            acc += double(row_exp(s2));
+            acc += double(row_exp(s3));
             bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) | (a + 2 != t && !isfinite(s2)) |
                    (a + 3 != t && !isfinite(s3));
         }
     } else {
         for (int64_t a = lane; a < len; a += kWave) {
             const float s = row[a] - m;
-            acc += double(expf(s));
+            acc += double(row_exp(s));
             bad |= (a != t && !isfinite(s));
         }
     }
@@ -298,14 +307,14 @@ __global__ __launch_bounds__(kBlock) void xent_backward_kernel(const float* __re
         for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
             const f4 v = ld4(row + a);
             f4 g;
-            g.x = scale * expf(v.x - m) + (a == t ? neg_c : -0.0f);
-            g.y = scale * expf(v.y - m) + (a + 1 == t ? neg_c : -0.0f);
-            g.z = scale * expf(v.z - m) + (a + 2 == t ? neg_c : -0.0f);
-            g.w = scale * expf(v.w - m) + (a + 3 == t ? neg_c : -0.0f);
+            g.x = scale * row_exp(v.x - m) + (a == t ? neg_c : -0.0f);
+            g.y = scale * row_exp(v.y - m) + (a + 1 == t ? neg_c : -0.0f);
+            g.z = scale * row_exp(v.z - m) + (a + 2 == t ? neg_c : -0.0f);
+            g.w = scale * row_exp(v.w - m) + (a + 3 == t ? neg_c : -0.0f);
             *reinterpret_cast<f4*>(out + a) = g;
         }
     } else {
-        for (int64_t a = lane; a < len; a += kWave) out[a] = scale * expf(row[a] - m) + (a == t ? neg_c : -0.0f);
+        for (int64_t a = lane; a < len; a += kWave) out[a] = scale * row_exp(row[a] - m) + (a == t ? neg_c : -0.0f);
     }
 }
 

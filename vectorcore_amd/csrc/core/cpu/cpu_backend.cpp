@@ -44,35 +44,40 @@ void binary_loop(const float* a, const Shape& a_shape, const Strides& a_strides,
         });
         return;
     }
-    // General broadcast: per output row, resolve both row starts, then walk the
-    // last axis with a step of 0 or the operand's last stride.
+    // General broadcast: each operand gets a stride per output axis (0 where
+    // it is broadcast). A chunk of the flat output decodes its first index
+    // once, then advances an odometer, carrying into the outer axes and
+    // moving both operand offsets by their strides.
     const std::size_t rank = out_shape.size();
-    const std::size_t inner = rank ? out_shape.back() : 1;
-    const std::size_t rows = count / inner;
-    auto step_of = [&](const Shape& s, const Strides& st) -> std::size_t {
-        return (rank == 0 || s.empty() || s.back() == 1) ? 0 : st.back();
+    std::vector<std::size_t> step_a(rank, 0), step_b(rank, 0);
+    const auto place = [&](const Shape& shape, const Strides& strides, std::vector<std::size_t>& step) {
+        const std::size_t lead = rank - shape.size();
+        for (std::size_t d = 0; d < shape.size(); ++d)
+            if (shape[d] != 1) step[lead + d] = strides[d];
     };
-    const std::size_t sa = step_of(a_shape, a_strides), sb = step_of(b_shape, b_strides);
-    parallel_for(rows, std::max<std::size_t>(1, kGrain / std::max<std::size_t>(inner, 1)),
-                 [&](std::size_t r0, std::size_t r1) {
-                     for (std::size_t r = r0; r < r1; ++r) {
-                         std::size_t rem = r, ao = 0, bo = 0;
-                         for (std::size_t ax = rank ? rank - 1 : 0; ax-- > 0;) {
-                             const std::size_t c = rem % out_shape[ax];
-                             rem /= out_shape[ax];
-                             if (ax + a_shape.size() >= rank) {
-                                 const std::size_t i = ax + a_shape.size() - rank;
-                                 if (a_shape[i] != 1) ao += c * a_strides[i];
-                             }
-                             if (ax + b_shape.size() >= rank) {
-                                 const std::size_t i = ax + b_shape.size() - rank;
-                                 if (b_shape[i] != 1) bo += c * b_strides[i];
-                             }
-                         }
-                         float* o = out + r * inner;
-                         for (std::size_t j = 0; j < inner; ++j) o[j] = f(a[ao + j * sa], b[bo + j * sb]);
-                     }
-                 });
+    place(a_shape, a_strides, step_a);
+    place(b_shape, b_strides, step_b);
+    parallel_for(count, kGrain, [&](std::size_t first, std::size_t last) {
+        std::vector<std::size_t> digit(rank, 0);
+        std::size_t oa = 0, ob = 0, rest = first;
+        for (std::size_t d = rank; d-- > 0;) {
+            digit[d] = rest % out_shape[d];
+            rest /= out_shape[d];
+            oa += digit[d] * step_a[d];
+            ob += digit[d] * step_b[d];
+        }
+        for (std::size_t i = first; i < last; ++i) {
+            out[i] = f(a[oa], b[ob]);
+            for (std::size_t d = rank; d-- > 0;) {  // next index: carry into outer axes
+                oa += step_a[d];
+                ob += step_b[d];
+                if (++digit[d] < out_shape[d]) break;
+                oa -= digit[d] * step_a[d];
+                ob -= digit[d] * step_b[d];
+                digit[d] = 0;
+            }
+        }
+    });
 }
 
 template <class F>
@@ -185,73 +190,106 @@ void transpose(const float* input, float* output, std::size_t batch, std::size_t
     });
 }
 
+namespace {
+
+constexpr std::size_t kSumChunk = std::size_t(1) << 16;
+
+// One chunk of the full sum. Element i of the chunk goes to lane i % 4 while
+// a whole group of four remains; the lanes are joined in lane order and the
+// leftover elements added after them: the rounding of the reference's CPU
+// sum (src/cpu/cpu_backend.cpp:392-418).
+double chunk_sum(const float* x, std::size_t n) {
+    double lane[4] = {0.0, 0.0, 0.0, 0.0};
+    const std::size_t whole = n - n % 4;
+    for (std::size_t g = 0; g < whole; g += 4)
+        for (int l = 0; l < 4; ++l) lane[l] += x[g + l];
+    double joined = ((lane[0] + lane[1]) + lane[2]) + lane[3];
+    for (std::size_t i = whole; i < n; ++i) joined += x[i];
+    return joined;
+}
+
+// Columns handled together by one task of an axis reduction: their running
+// values stay in a stack array while the task walks the reduced axis.
+constexpr std::size_t kColumnBlock = 512;
+
+}  // namespace
+
 float sum(const float* input, std::size_t count) {
-    // 65536-element chunks, each with four double accumulators; chunk results
-    // joined in chunk order, so the value is independent of the thread count.
-    constexpr std::size_t kChunk = std::size_t(1) << 16;
-    const std::size_t chunks = (count + kChunk - 1) / kChunk;
-    std::vector<double> part(chunks, 0.0);
+    // Fixed 65536-element chunks, joined in chunk order: the same value for
+    // any number of threads.
+    const std::size_t chunks = (count + kSumChunk - 1) / kSumChunk;
+    std::vector<double> chunk_total(chunks);
     parallel_for(chunks, 1, [&](std::size_t c0, std::size_t c1) {
         for (std::size_t c = c0; c < c1; ++c) {
-            const std::size_t i0 = c * kChunk, i1 = std::min(count, i0 + kChunk);
-            double s0 = 0, s1 = 0, s2 = 0, s3 = 0;
-            std::size_t i = i0;
-            for (; i + 4 <= i1; i += 4) {
-                s0 += input[i];
-                s1 += input[i + 1];
-                s2 += input[i + 2];
-                s3 += input[i + 3];
-            }
-            double t = s0 + s1 + s2 + s3;
-            for (; i < i1; ++i) t += input[i];
-            part[c] = t;
+            const std::size_t begin = c * kSumChunk;
+            chunk_total[c] = chunk_sum(input + begin, std::min(kSumChunk, count - begin));
         }
     });
     double total = 0.0;
-    for (double p : part) total += p;
+    for (std::size_t c = 0; c < chunks; ++c) total += chunk_total[c];
     return static_cast<float>(total);
 }
 
 void reduce_axis(const float* input, float* output, std::size_t outer, std::size_t length, std::size_t inner,
                  ReduceOp operation) {
     if (length == 0 && operation != ReduceOp::Sum) throw std::invalid_argument("max/argmax over an empty axis is undefined");
-    const std::size_t grain = std::max<std::size_t>(1, kGrain / std::max<std::size_t>(length * inner, 1));
-    parallel_for(outer, grain, [&](std::size_t o0, std::size_t o1) {
-        std::vector<double> acc;
-        std::vector<float> best;
-        std::vector<std::size_t> idx;
-        for (std::size_t o = o0; o < o1; ++o) {
-            const float* base = input + o * length * inner;
-            float* dst = output + o * inner;
+    // Tasks are (outer index, block of up to kColumnBlock columns), so even a
+    // single outer index (a bias gradient) spreads over the threads. Every
+    // output is a sequential walk along the axis from index 0, as in the
+    // reference: a double sum, or the first strict maximum.
+    const std::size_t blocks = (inner + kColumnBlock - 1) / kColumnBlock;
+    const std::size_t work = std::max<std::size_t>(1, length * std::min(inner, kColumnBlock));
+    parallel_for(outer * blocks, std::max<std::size_t>(1, kGrain / work), [&](std::size_t t0, std::size_t t1) {
+        double total[kColumnBlock];
+        float top[kColumnBlock];
+        std::size_t where[kColumnBlock];
+        for (std::size_t t = t0; t < t1; ++t) {
+            const std::size_t o = t / blocks, c0 = (t % blocks) * kColumnBlock;
+            const std::size_t width = std::min(kColumnBlock, inner - c0);
+            const float* column = input + o * length * inner + c0;
+            float* dst = output + o * inner + c0;
             if (operation == ReduceOp::Sum) {
-                acc.assign(inner, 0.0);
-                for (std::size_t a = 0; a < length; ++a)
-                    for (std::size_t i = 0; i < inner; ++i) acc[i] += base[a * inner + i];
-                for (std::size_t i = 0; i < inner; ++i) dst[i] = static_cast<float>(acc[i]);
+                std::fill(total, total + width, 0.0);
+                for (std::size_t a = 0; a < length; ++a, column += inner)
+                    for (std::size_t j = 0; j < width; ++j) total[j] += column[j];
+                for (std::size_t j = 0; j < width; ++j) dst[j] = static_cast<float>(total[j]);
                 continue;
             }
-            best.assign(base, base + inner);
-            idx.assign(inner, 0);
-            for (std::size_t a = 1; a < length; ++a)
-                for (std::size_t i = 0; i < inner; ++i)
-                    if (base[a * inner + i] > best[i]) {  // strict: the first maximum wins
-                        best[i] = base[a * inner + i];
-                        idx[i] = a;
-                    }
-            for (std::size_t i = 0; i < inner; ++i)
-                dst[i] = operation == ReduceOp::Max ? best[i] : static_cast<float>(idx[i]);
+            for (std::size_t j = 0; j < width; ++j) {
+                top[j] = column[j];
+                where[j] = 0;
+            }
+            for (std::size_t a = 1; a < length; ++a) {
+                column += inner;
+                for (std::size_t j = 0; j < width; ++j) {
+                    if (!(column[j] > top[j])) continue;  // a later equal value or NaN never replaces
+                    top[j] = column[j];
+                    where[j] = a;
+                }
+            }
+            for (std::size_t j = 0; j < width; ++j)
+                dst[j] = operation == ReduceOp::Max ? top[j] : static_cast<float>(where[j]);
         }
     });
 }
 
 void scatter_axis(const float* values, const float* indices, float* output, std::size_t outer, std::size_t length,
                   std::size_t inner) {
-    std::fill(output, output + outer * length * inner, 0.0F);
-    for (std::size_t o = 0; o < outer; ++o)
-        for (std::size_t i = 0; i < inner; ++i) {
-            const auto a = static_cast<std::size_t>(indices[o * inner + i]);
-            output[(o * length + a) * inner + i] = values[o * inner + i];
-        }
+    // Written as a gather: output element (o, a, i) takes the value of
+    // column (o, i) when that column's index is a, else 0, so each output
+    // element is written once and the pass runs in parallel.
+    const std::size_t slab = length * inner;
+    parallel_for(outer * length, std::max<std::size_t>(1, kGrain / std::max<std::size_t>(inner, 1)),
+                 [&](std::size_t r0, std::size_t r1) {
+                     for (std::size_t r = r0; r < r1; ++r) {
+                         const std::size_t o = r / length, a = r % length;
+                         const float* v = values + o * inner;
+                         const float* idx = indices + o * inner;
+                         float* dst = output + o * slab + a * inner;
+                         for (std::size_t i = 0; i < inner; ++i)
+                             dst[i] = static_cast<std::size_t>(idx[i]) == a ? v[i] : 0.0F;
+                     }
+                 });
 }
 
 }  // namespace vectorcore::cpu

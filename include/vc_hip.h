@@ -205,6 +205,20 @@ int vc_hip_reduce_sum(const float* in, size_t count, float* out);
  * argmax return the first maximum (argmax as a float index), and a NaN first
  * element wins, as in src/cpu/cpu_backend.cpp:443-457. */
 int vc_hip_reduce_axis(const float* in, float* out, size_t outer, size_t length, size_t inner, int op);
+/* vc_hip_reduce_axis without any device allocation: the same kernels, the
+ * same results bit for bit, with the partial results (column sums, max and
+ * argmax splits) in a static 2 MiB device array (one per GPU, held until the
+ * process ends) instead of pool memory. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code recorded into a HIP
+ * graph, tight serving loops, harnesses that forbid allocation). 2 MiB holds
+ * the column sums of up to 2^17 outputs (a [8192, 4096] bias gradient needs
+ * 1 MiB) and the max/argmax splits of long axes with few outputs; a call that
+ * needs more fails with VC_HIP_ERR_INVALID_ARGUMENT before launching
+ * anything. Row and one-thread-per-output reductions need no partial results.
+ * Calls are serialised
+ * by the library and run in order on its one stream, so consecutive calls
+ * reuse the array safely; nothing in it needs to start at zero. */
+int vc_hip_reduce_axis_noalloc(const float* in, float* out, size_t outer, size_t length, size_t inner, int op);
 /* MetalBackend::scatter_axis (metal_backend.hpp:49-51). */
 int vc_hip_scatter_axis(const float* values, const float* indices, float* out, size_t outer, size_t length,
                         size_t inner);

@@ -62,6 +62,7 @@ _SIGNATURES = {
     "vc_hip_transpose_last2": ([_vp, _vp, _sz, _sz, _sz], _i),
     "vc_hip_reduce_sum": ([_vp, _sz, _vp], _i),
     "vc_hip_reduce_axis": ([_vp, _vp, _sz, _sz, _sz, _i], _i),
+    "vc_hip_reduce_axis_noalloc": ([_vp, _vp, _sz, _sz, _sz, _i], _i),
     "vc_hip_scatter_axis": ([_vp, _vp, _vp, _sz, _sz, _sz], _i),
     "vc_hip_xent_forward": ([_vp, _vp, _sz, _sz, _vp, _vp], _i),
     "vc_hip_xent_backward": ([_vp, _vp, _vp, _vp, _sz, _sz, _vp], _i),

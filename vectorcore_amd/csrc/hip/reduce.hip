@@ -19,6 +19,8 @@
 #include <algorithm>
 #include <limits>
 #include <memory>
+#include <mutex>
+#include <string>
 #include <vector>
 
 namespace vchip {
@@ -463,6 +465,58 @@ void reduce_axis(const float* in, float* out, int64_t outer, int64_t len, int64_
     p.done();
 }
 
+// ---- partial results without allocation (vc_hip_reduce_axis_noalloc) ------------
+// A file-scope device array holds the partial results of the
+// allocation-free entry point; each GPU that loads the library holds its own
+// copy until the process ends. On the host, `scratch` names a stand-in, not
+// device memory: host code uses only the address that hipGetSymbolAddress
+// returns for the current device. A column sum keeps segs * outputs at most
+// 2048 * 64 + outputs (double partials), so 2 MiB holds the column sums of up
+// to 2^17 outputs: the bias gradient of a [8192, 4096] layer needs 1 MiB. A
+// max/argmax split over a long axis with few outputs needs 8 bytes per
+// (segment, output); a shape that needs more than the array is rejected.
+constexpr size_t kNoAllocScratchBytes = size_t(2) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+
+// The address of this device's copy of `scratch`, resolved once per device
+// with that device current.
+void* noalloc_scratch(const Device& d) {
+    static std::mutex mu;
+    static void* address[kMaxDevices] = {};
+    if (d.ordinal < 0 || d.ordinal >= kMaxDevices) fail(VC_HIP_ERR_RUNTIME, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (!address[d.ordinal]) {
+        void* p = nullptr;
+        check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (reduction scratch)");
+        if (!p) fail(VC_HIP_ERR_RUNTIME, "hipGetSymbolAddress returned no address for the reduction scratch");
+        address[d.ordinal] = p;
+    }
+    return address[d.ordinal];
+}
+
+// Hands out 256-byte-aligned pieces of the static array, in order; fails,
+// before anything is launched, when a call needs more than it holds.
+class StaticPartials final : public PartialMemory {
+public:
+    explicit StaticPartials(void* base) : base_(static_cast<char*>(base)) {}
+    void* take(size_t bytes) override {
+        const size_t begin = (used_ + 255) / 256 * 256;
+        if (bytes > kNoAllocScratchBytes || begin > kNoAllocScratchBytes - bytes)
+            fail(VC_HIP_ERR_INVALID_ARGUMENT,
+                 "vc_hip_reduce_axis_noalloc: this reduction needs " + std::to_string(begin + bytes) +
+                     " bytes of partial results; the allocation-free entry point holds " +
+                     std::to_string(kNoAllocScratchBytes) + " (use vc_hip_reduce_axis)");
+        used_ = begin + bytes;
+        return base_ + begin;
+    }
+
+private:
+    char* base_;
+    size_t used_ = 0;
+};
+
 }  // namespace
 }  // namespace vchip
 
@@ -498,6 +552,19 @@ int vc_hip_reduce_sum(const float* in, size_t count, float* out) {
 int vc_hip_reduce_axis(const float* in, float* out, size_t outer, size_t length, size_t inner, int op) {
     return guard([&] {
         PoolPartials memory;
+        reduce_axis(in, out, int64_t(outer), int64_t(length), int64_t(inner), op, memory);
+    });
+}
+
+int vc_hip_reduce_axis_noalloc(const float* in, float* out, size_t outer, size_t length, size_t inner, int op) {
+    return guard([&] {
+        Device& d = require_device();
+        // One call at a time fills the array and enqueues the kernels that
+        // read it; the library's single in-order stream then runs calls one
+        // after another, so a call never sees another's partial results.
+        static std::mutex serial;
+        std::lock_guard<std::mutex> lock(serial);
+        StaticPartials memory(noalloc_scratch(d));
         reduce_axis(in, out, int64_t(outer), int64_t(length), int64_t(inner), op, memory);
     });
 }

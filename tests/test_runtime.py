@@ -927,3 +927,14 @@ def test_invalid_inputs_raise(call):
 
 def test_sum_of_empty_axis_is_zero(device):
     close(vc.Tensor(np.zeros((2, 0), dtype=np.float32), device=device).sum(1), [0.0, 0.0])
+
+
+def test_reference_module_name_is_the_same_module():
+    # The reference's tests and examples start with `import vectorcore as vc`
+    # (python/bindings.cpp:63).
+    import vectorcore
+    assert vectorcore.Tensor is vc.Tensor and vectorcore.cross_entropy is vc.cross_entropy
+    assert vectorcore.Linear is vc.Linear and vectorcore.sgd_step is vc.sgd_step
+    x = vectorcore.Tensor([1.0, 2.0, 3.0], requires_grad=True)
+    ((x * x) + x).sum().backward()
+    np.testing.assert_array_equal(x.grad.numpy(), [3, 5, 7])

@@ -1,8 +1,13 @@
 """In-tree build of the native parts of vectorcore_amd.
 
-  libvc_hip.so   HIP kernels + the C ABI of include/vc_hip.h, for gfx950
-  _vectorcore*.so  the C++20 tensor/autograd runtime and its pybind11 module,
-                 linked against libvc_hip.so (rpath $ORIGIN)
+  libvc_hip.so      HIP kernels + the C ABI of include/vc_hip.h, for gfx950
+  libvectorcore.so  the C++20 tensor/autograd runtime (the reference's C++
+                    API with the hip device), linked against libvc_hip.so
+  _vectorcore*.so   the pybind11 module over libvectorcore.so (rpath $ORIGIN)
+  _build/bin/test_vectorcore, _build/asan/..., _build/tsan/...
+                    the C++ suite (tests/cpp), linked against the library and,
+                    for the sanitizer builds, compiled together with the
+                    runtime's sources under ASan+UBSan or TSan
 
 Run `python vectorcore_amd/build.py` (or __graft_entry__.build()). Every call
 recompiles; objects go to vectorcore_amd/_build/, libraries next to this file.
@@ -25,8 +30,14 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["runtime.hip", "elementwise.hip", "reduce.hip", "xent.hip", "gemm.hip"]
-CORE_SOURCES = ["shape.cpp", "storage.cpp", "tensor.cpp", "autograd.cpp", "ops.cpp", "nn.cpp",
-                "cpu/parallel.cpp", "cpu/cpu_backend.cpp", "hip/hip_backend.cpp", "python/bindings.cpp"]
+LIB_SOURCES = ["shape.cpp", "storage.cpp", "tensor.cpp", "autograd.cpp", "ops.cpp", "nn.cpp",
+               "cpu/parallel.cpp", "cpu/cpu_backend.cpp", "hip/hip_backend.cpp"]
+BINDINGS = "python/bindings.cpp"
+CPP_TEST = ROOT / "tests" / "cpp" / "test_vectorcore.cpp"
+ORACLE_C = ROOT / "oracle" / "vc_oracle.c"
+# Sanitizer variants of the C++ suite: (directory under _build, compile and link flags).
+SANITIZERS = {"asan": ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer"],
+              "tsan": ["-fsanitize=thread"]}
 
 # hipcc flags. Packed FP32 instructions are disabled (they are not trusted on
 # this hardware pool); floating-point contraction is off so elementwise
@@ -72,35 +83,82 @@ def _python_includes() -> list[str]:
     return ["-I", sysconfig.get_paths()["include"], "-I", pybind11.get_include()]
 
 
+def _core_flags() -> list[str]:
+    return ["-std=c++20", "-fPIC", "-Wall", "-Wextra", "-I", str(CSRC / "core" / "include"), "-I", str(ROOT / "include")]
+
+
 def build_core(verbose: bool = False) -> Path:
-    """Compile the C++ runtime + bindings into the _vectorcore extension module."""
-    OBJ.mkdir(exist_ok=True)
-    (OBJ / "cpu").mkdir(exist_ok=True)
-    (OBJ / "hip").mkdir(exist_ok=True)
-    (OBJ / "python").mkdir(exist_ok=True)
-    flags = ["g++", "-std=c++20", "-O3", "-DNDEBUG", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wextra",
-             "-I", str(CSRC / "core" / "include"), "-I", str(ROOT / "include"), *_python_includes()]
+    """Compile the C++ runtime into libvectorcore.so and its bindings into the _vectorcore module."""
+    for sub in ("cpu", "hip", "python"):
+        (OBJ / sub).mkdir(parents=True, exist_ok=True)
+    flags = ["g++", "-O3", "-DNDEBUG", *_core_flags()]
 
     def compile_one(src: str) -> Path:
         obj = OBJ / (src.replace(".cpp", ".o"))
-        log = _run(flags + ["-c", str(CSRC / "core" / src), "-o", str(obj)])
+        extra = ["-fvisibility=hidden", *_python_includes()] if src == BINDINGS else []
+        log = _run(flags + extra + ["-c", str(CSRC / "core" / src), "-o", str(obj)])
         if verbose and log:
             print(log, file=sys.stderr)
         return obj
 
-    objs = _parallel(compile_one, CORE_SOURCES)
+    objs = _parallel(compile_one, LIB_SOURCES + [BINDINGS])
+    lib = PKG / "libvectorcore.so"
+    tmp = lib.with_suffix(".so.tmp")
+    _run(["g++", "-shared", "-o", str(tmp), *map(str, objs[:-1]), "-L", str(PKG), "-lvc_hip", "-Wl,-rpath,$ORIGIN",
+          "-lpthread"])
+    tmp.replace(lib)
     suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
     out = PKG / f"_vectorcore{suffix}"
     tmp = out.with_name(out.name + ".tmp")
-    _run(["g++", "-shared", "-o", str(tmp), *map(str, objs), "-L", str(PKG), "-lvc_hip",
+    _run(["g++", "-shared", "-o", str(tmp), str(objs[-1]), "-L", str(PKG), "-lvectorcore", "-lvc_hip",
           "-Wl,-rpath,$ORIGIN", "-lpthread"])
     tmp.replace(out)
     return out
 
 
-def build_all(verbose: bool = False) -> None:
+def build_cpp_tests(sanitizers: bool = True) -> list[Path]:
+    """The C++ suite against libvectorcore.so, and (sanitizers=True) its ASan+UBSan and TSan builds,
+    which compile the runtime's sources and the oracle's C kernels with the sanitizer."""
+    built = []
+    bindir = OBJ / "bin"
+    bindir.mkdir(parents=True, exist_ok=True)
+    oracle_obj = bindir / "vc_oracle.o"
+    # The oracle's C kernels, serial (no OpenMP), as the suite's cross-check.
+    _run(["gcc", "-std=c11", "-O2", "-ffp-contract=off", "-c", str(ORACLE_C), "-o", str(oracle_obj)])
+    exe = bindir / "test_vectorcore"
+    _run(["g++", "-O2", *_core_flags(), "-I", str(ORACLE_C.parent), str(CPP_TEST), str(oracle_obj), "-o", str(exe),
+          "-L", str(PKG), "-lvectorcore", "-lvc_hip", "-Wl,-rpath,$ORIGIN/../..", "-lpthread", "-lm"])
+    built.append(exe)
+    if not sanitizers:
+        return built
+
+    def compile_variant(item: tuple[str, str]) -> Path:
+        name, src = item
+        obj = OBJ / name / src.replace(".cpp", ".o").replace(".c", ".o")
+        obj.parent.mkdir(parents=True, exist_ok=True)
+        if src.endswith(".c"):
+            _run(["gcc", "-std=c11", "-O1", "-g", *SANITIZERS[name], "-ffp-contract=off", "-c", str(ORACLE_C),
+                  "-o", str(obj)])
+        else:
+            _run(["g++", "-O1", "-g", *SANITIZERS[name], *_core_flags(), "-c", str(CSRC / "core" / src), "-o", str(obj)])
+        return obj
+
+    jobs = [(name, src) for name in SANITIZERS for src in LIB_SOURCES + ["vc_oracle.c"]]
+    objs = dict(zip(jobs, _parallel(compile_variant, jobs)))
+    for name, san in SANITIZERS.items():
+        out = OBJ / name / "test_vectorcore"
+        _run(["g++", "-O1", "-g", *san, *_core_flags(), "-I", str(ORACLE_C.parent), str(CPP_TEST),
+              *[str(objs[(name, src)]) for src in LIB_SOURCES + ["vc_oracle.c"]], "-o", str(out), "-L", str(PKG),
+              "-lvc_hip", "-Wl,-rpath,$ORIGIN/../..", "-lpthread", "-lm"])
+        built.append(out)
+    return built
+
+
+def build_all(verbose: bool = False, cpp_tests: bool = True) -> None:
     build_hip(verbose)
     build_core(verbose)
+    if cpp_tests:
+        build_cpp_tests()
 
 
 if __name__ == "__main__":

@@ -28,6 +28,19 @@ namespace {
     throw std::runtime_error("Metal is unavailable: VectorCore was built without Apple Metal");
 }
 
+// A rule's two gradients as one vector. Both are complete objects before the
+// vector is built, so when computing the second throws (a version check),
+// the first is destroyed; a brace-initialised vector built from the two
+// expressions leaks the first under GCC 11, which does not destroy the
+// already-built elements of a partly built initializer list.
+std::vector<Tensor> two_grads(Tensor first, Tensor second) {
+    std::vector<Tensor> out;
+    out.reserve(2);
+    out.push_back(std::move(first));
+    out.push_back(std::move(second));
+    return out;
+}
+
 HipBackend& hip() { return HipBackend::instance(); }
 const Storage& st(const Tensor& t) { return *t.impl()->storage; }
 std::size_t off(const Tensor& t) { return t.impl()->offset; }
@@ -244,7 +257,7 @@ Tensor add(const Tensor& a, const Tensor& b) {
     const Shape as = a.shape(), bs = b.shape();
     const bool na = a.requires_grad(), nb = b.requires_grad();
     detail::attach_grad_fn(out, {a, b}, [=](const Tensor& g) {
-        return std::vector<Tensor>{na ? detail::sum_to_shape(g, as) : Tensor(), nb ? detail::sum_to_shape(g, bs) : Tensor()};
+        return two_grads(na ? detail::sum_to_shape(g, as) : Tensor(), nb ? detail::sum_to_shape(g, bs) : Tensor());
     });
     return out;
 }
@@ -254,7 +267,7 @@ Tensor subtract(const Tensor& a, const Tensor& b) {
     const Shape as = a.shape(), bs = b.shape();
     const bool na = a.requires_grad(), nb = b.requires_grad();
     detail::attach_grad_fn(out, {a, b}, [=](const Tensor& g) {
-        return std::vector<Tensor>{na ? detail::sum_to_shape(g, as) : Tensor(), nb ? detail::sum_to_shape(-g, bs) : Tensor()};
+        return two_grads(na ? detail::sum_to_shape(g, as) : Tensor(), nb ? detail::sum_to_shape(-g, bs) : Tensor());
     });
     return out;
 }
@@ -265,8 +278,8 @@ Tensor multiply(const Tensor& a, const Tensor& b) {
     const bool na = a.requires_grad(), nb = b.requires_grad();
     const detail::SavedTensor sa(a), sb(b);
     detail::attach_grad_fn(out, {a, b}, [=](const Tensor& g) {
-        return std::vector<Tensor>{na ? detail::sum_to_shape(g * sb.unpack(), as) : Tensor(),
-                                   nb ? detail::sum_to_shape(g * sa.unpack(), bs) : Tensor()};
+        return two_grads(na ? detail::sum_to_shape(g * sb.unpack(), as) : Tensor(),
+                                   nb ? detail::sum_to_shape(g * sa.unpack(), bs) : Tensor());
     });
     return out;
 }

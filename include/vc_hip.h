@@ -177,6 +177,19 @@ int vc_hip_matmul(const float* a, const float* b, float* c, size_t m, size_t k, 
 int vc_hip_matmul_relu_mask(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
                             const size_t* a_offsets, const size_t* b_offsets, size_t batch, int trans_a, int trans_b,
                             const float* mask);
+/* vc_hip_matmul_relu_mask for one product (batch 1), which also writes the
+ * column sums of c: column_sum[j] = sum_i c[i][j], accumulated in double in a
+ * fixed order and rounded once to float. c is the same bits as
+ * vc_hip_matmul_relu_mask's. The sums come from per-tile partials in the
+ * product's epilogue and one small combining pass, so c is not read again.
+ * No counterpart in the reference: it serves the backward of
+ * relu(x @ W + b) where the ReLU's upstream gradient comes from a product
+ * (src/ops.cpp:252-260, 395-403), whose add rule (src/ops.cpp:98-109) then
+ * reduces that gradient to the bias's shape with sum_to_shape
+ * (src/autograd.cpp:50-72), i.e. a column sum in double (reduce_axis,
+ * src/cpu/cpu_backend.cpp:420-441). k must be > 0 unless m is 0. */
+int vc_hip_matmul_relu_mask_colsum(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                                   int trans_a, int trans_b, const float* mask, float* column_sum);
 /* A forward layer in one kernel: c = a @ b (+ bias[column]) (then ReLU),
  * a [m][k], b [k][n], bias [n] or null, all contiguous; relu nonzero applies
  * x > 0 ? x : 0 after the bias. The same bits as vc_hip_matmul, then the
@@ -212,7 +225,7 @@ int vc_hip_reduce_axis(const float* in, float* out, size_t outer, size_t length,
  * is for callers that cannot allocate device memory (code recorded into a HIP
  * graph, tight serving loops, harnesses that forbid allocation). 2 MiB holds
  * the column sums of up to 2^17 outputs (a [8192, 4096] bias gradient needs
- * 1 MiB) and the max/argmax splits of long axes with few outputs; a call that
+ * 256 KiB) and the max/argmax splits of long axes with few outputs; a call that
  * needs more fails with VC_HIP_ERR_INVALID_ARGUMENT before launching
  * anything. Row and one-thread-per-output reductions need no partial results.
  * Calls are serialised
@@ -240,6 +253,20 @@ int vc_hip_xent_backward(const float* logits, const int32_t* targets, const floa
  * value (src/tensor.cpp:244-249), which then needs no upload. */
 int vc_hip_xent_backward_value(const float* logits, const int32_t* targets, const float* row_stats,
                                float grad_loss, size_t rows, size_t classes, float* grad_logits);
+
+/* vc_hip_xent_backward (grad_loss a device scalar) or
+ * vc_hip_xent_backward_value (grad_loss NULL: grad_loss_value), which also
+ * writes the column sums of grad_logits: column_sum[j] = sum_i
+ * grad_logits[i][j], accumulated in double in a fixed order and rounded once.
+ * grad_logits has the same bits as those entry points'. No counterpart in the
+ * reference: it serves a loss on logits = h @ W + b, whose add rule
+ * (src/ops.cpp:98-109) reduces the logits' gradient to the bias's shape with
+ * sum_to_shape (src/autograd.cpp:50-72), a column sum in double
+ * (src/cpu/cpu_backend.cpp:420-441); here it comes from per-row-block
+ * partials the backward kernel keeps while writing grad_logits. */
+int vc_hip_xent_backward_colsum(const float* logits, const int32_t* targets, const float* row_stats,
+                                const float* grad_loss, float grad_loss_value, size_t rows, size_t classes,
+                                float* grad_logits, float* column_sum);
 
 /* ---- measurement ------------------------------------------------------------- */
 /* When enabled, the kernels of each labelled entry-point call carry HIP

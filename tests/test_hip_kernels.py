@@ -125,6 +125,50 @@ def test_gemm_relu_mask_is_gemm_then_relu_backward_bitexact(gemm_kernel):
             assert (fused.numpy() == 0).any() and (fused.numpy() != 0).any()
 
 
+@pytest.mark.parametrize("m,k,n", [(300, 257, 130), (128, 64, 200), (100, 70, 33), (4096, 512, 1000),
+                                   (2048, 4096, 64), (8192, 1000, 4096)])
+def test_masked_product_with_column_sums(gemm_kernel, m, k, n):
+    """vc_hip_matmul_relu_mask_colsum: the product is vc_hip_matmul_relu_mask's
+    bits, and the column sums equal the reduction of that product (the
+    oracle's sequential double sum) to the last bit or within 1e-6. Covers
+    full and partial 128-row tiles, one tile, no full tile, a split-K shape
+    (2048 x 4096 x 64: the sums come from a separate reduction) and the
+    portable kernel (the same)."""
+    rng = np.random.default_rng(m + k + n)
+    a = rng.uniform(-1, 1, size=(m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, size=(n, k)).astype(np.float32)
+    x = rng.standard_normal((m, n)).astype(np.float32)
+    x.flat[:4] = [0.0, -0.0, np.nan, np.inf]
+    da, db, dx = C.Buffer.of(a), C.Buffer.of(b), C.Buffer.of(x)
+    fused, plain, sums = C.Buffer((m, n)), C.Buffer((m, n)), C.Buffer((n,))
+    C.check(C.lib().vc_hip_matmul_relu_mask_colsum(da.ptr, db.ptr, fused.ptr, m, k, n, 0, 1, dx.ptr, sums.ptr))
+    C.check(C.lib().vc_hip_matmul_relu_mask(da.ptr, db.ptr, plain.ptr, m, k, n, C.sizes([0]), C.sizes([0]), 1, 0, 1,
+                                            dx.ptr))
+    product = plain.numpy()
+    np.testing.assert_array_equal(fused.numpy(), product)
+    want = K.reduce_axis(product, 0, K.SUM)
+    got = sums.numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6 * np.abs(product).sum(0).max())
+    assert (got == want).mean() > 0.99
+
+
+def test_column_sums_leave_out_rows_past_the_matrix():
+    # An infinity in B makes the padded rows of the last tile NaN (0 * inf);
+    # those rows are not part of C and must not reach the sums.
+    rng = np.random.default_rng(5)
+    m, k, n = 200, 64, 96  # one full tile of rows, then 72 rows of a partial tile
+    a = rng.uniform(0.5, 1, size=(m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, size=(n, k)).astype(np.float32)
+    b[7, 3] = np.inf
+    x = np.ones((m, n), np.float32)
+    da, db, dx = C.Buffer.of(a), C.Buffer.of(b), C.Buffer.of(x)
+    out, sums = C.Buffer((m, n)), C.Buffer((n,))
+    C.check(C.lib().vc_hip_matmul_relu_mask_colsum(da.ptr, db.ptr, out.ptr, m, k, n, 0, 1, dx.ptr, sums.ptr))
+    got, product = sums.numpy(), out.numpy()
+    assert np.isposinf(got[7]) and np.isposinf(product[:, 7]).all()
+    np.testing.assert_allclose(np.delete(got, 7), np.delete(K.reduce_axis(product, 0, K.SUM), 7), rtol=1e-6)
+
+
 def test_large_nn_product_runs_as_nt_on_a_transposed_copy_with_the_same_bits():
     """From 4096 rows an NN product transposes B and runs the NT kernel; the
     LDS tiles, and so the bits, are those of NN on B as stored. Shapes below
@@ -452,6 +496,34 @@ def test_cross_entropy_register_and_streaming_paths_agree():
                                                    classes, g.ptr))
         grads.append(g.numpy())
     np.testing.assert_array_equal(grads[1], grads[0])
+
+
+@pytest.mark.parametrize("rows,classes", [(8192, 1000), (17, 1000), (300, 37), (100, 3000), (64, 2048), (5, 4)])
+def test_cross_entropy_backward_with_column_sums(rows, classes):
+    """vc_hip_xent_backward_colsum: the gradient is the plain backward's bits
+    and the column sums equal the oracle's reduction of that gradient. 37
+    classes (not a multiple of 4) and 3000 (beyond the register-held rows)
+    take the plain kernel and a separate reduction; 17 rows leave the last
+    row block short."""
+    xe = W.xent(rows=rows, classes=classes, seed=rows + classes)
+    logits, targets = xe["logits"], xe["targets"].astype(np.int32)
+    dl, dt = C.Buffer.of(logits), C.Buffer.of(targets, dtype=np.int32)
+    stats, loss = C.Buffer((rows, 2)), C.Buffer((1,))
+    C.check(C.lib().vc_hip_xent_forward(dl.ptr, dt.ptr, rows, classes, stats.ptr, loss.ptr))
+    seed = C.Buffer.of(np.array([0.75], np.float32))
+    for device_seed in (False, True):
+        plain, fused, sums = C.Buffer((rows, classes)), C.Buffer((rows, classes)), C.Buffer((classes,))
+        C.check(C.lib().vc_hip_xent_backward_value(dl.ptr, dt.ptr, stats.ptr, ctypes.c_float(0.75), rows, classes,
+                                                   plain.ptr))
+        C.check(C.lib().vc_hip_xent_backward_colsum(dl.ptr, dt.ptr, stats.ptr, seed.ptr if device_seed else None,
+                                                    ctypes.c_float(0.0 if device_seed else 0.75), rows, classes,
+                                                    fused.ptr, sums.ptr))
+        grad = plain.numpy()
+        np.testing.assert_array_equal(fused.numpy(), grad)
+        want = K.reduce_axis(grad, 0, K.SUM)
+        got = sums.numpy()
+        np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6 * np.abs(grad).sum(0).max())
+        assert (got == want).mean() > 0.99
 
 
 def _special_rows(classes, rng):

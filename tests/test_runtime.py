@@ -362,6 +362,53 @@ def test_relu_fold_gives_the_unfolded_bits(gemm_device):
     assert (npy(h.grad) != 0).sum() > (npy(h) > 0).sum()
 
 
+@hip_only
+def test_bias_gradients_come_from_the_producing_kernels():
+    # In cross_entropy(relu(x @ W1 + b1) @ W2 + b2) the product giving
+    # dz1 = (dy W2^T) * [z1 > 0] also leaves dz1's column sums, and the
+    # cross-entropy backward leaves those of dlogits; b1's and b2's add rules
+    # take them instead of reducing dz1 and dlogits again. The values equal
+    # the unfused path's (retained gradients turn both off) and the cpu
+    # device's.
+    rng = np.random.default_rng(41)
+    xs = rng.standard_normal((1000, 200)).astype(np.float32)
+    w1s = (rng.standard_normal((200, 300)) * 0.1).astype(np.float32)
+    b1s = (rng.standard_normal(300) * 0.1).astype(np.float32)
+    w2s = (rng.standard_normal((300, 52)) * 0.1).astype(np.float32)
+    b2s = (rng.standard_normal(52) * 0.1).astype(np.float32)
+
+    def grads(device, retain=False, profile=False):
+        x = T(xs, device)
+        w1, b1, w2, b2 = (T(v, device, True) for v in (w1s, b1s, w2s, b2s))
+        h = (x @ w1 + b1).relu()
+        logits = h @ w2 + b2
+        if retain:
+            h.retain_grad()
+            logits.retain_grad()
+        if profile:
+            vc.synchronize()
+            vc.hip_profile_reset()
+            vc.hip_profile(True, labels=["column_sum_combine", "reduce_axis_sum"])
+        vc.cross_entropy(logits, [i % 52 for i in range(1000)]).backward()
+        out = [npy(p.grad) for p in (w1, b1, w2, b2)]
+        if profile:
+            vc.hip_profile(False)
+            return out, vc.hip_profile_read()
+        return out
+
+    fused, prof = grads("hip", profile=True)
+    assert prof.get("column_sum_combine", {}).get("launches", 0) == 2, prof
+    assert "reduce_axis_sum" not in prof, prof  # no separate reduction of dz1 or dlogits
+    plain = grads("hip", retain=True)
+    for k in (1, 3):
+        np.testing.assert_allclose(fused[k], plain[k], rtol=1e-6, atol=1e-9)
+        assert (fused[k] == plain[k]).mean() > 0.99
+    for k in (0, 2):
+        np.testing.assert_array_equal(fused[k], plain[k])
+    for f, c in zip(fused, grads("cpu")):
+        np.testing.assert_allclose(f, c, rtol=1e-4, atol=1e-6)
+
+
 def test_relu_fold_with_a_shared_activation(device):
     _, got = _relu_net(device, reuse=True)
     _, cpu = _relu_net("cpu", reuse=True)

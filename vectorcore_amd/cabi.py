@@ -57,6 +57,7 @@ _SIGNATURES = {
     "vc_hip_div_backward": ([_vp, _vp, _szp, _szp, _sz, _vp, _szp, _szp, _sz, _szp, _sz, _vp, _vp], _i),
     "vc_hip_matmul": ([_vp, _vp, _vp, _sz, _sz, _sz, _szp, _szp, _sz, _i, _i], _i),
     "vc_hip_matmul_relu_mask": ([_vp, _vp, _vp, _sz, _sz, _sz, _szp, _szp, _sz, _i, _i, _vp], _i),
+    "vc_hip_matmul_relu_mask_colsum": ([_vp, _vp, _vp, _sz, _sz, _sz, _i, _i, _vp, _vp], _i),
     "vc_hip_matmul_bias_relu": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp, _i], _i),
     "vc_hip_matmul_reduce": ([_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _i], _i),
     "vc_hip_transpose_last2": ([_vp, _vp, _sz, _sz, _sz], _i),
@@ -67,6 +68,7 @@ _SIGNATURES = {
     "vc_hip_xent_forward": ([_vp, _vp, _sz, _sz, _vp, _vp], _i),
     "vc_hip_xent_backward": ([_vp, _vp, _vp, _vp, _sz, _sz, _vp], _i),
     "vc_hip_xent_backward_value": ([_vp, _vp, _vp, _f, _sz, _sz, _vp], _i),
+    "vc_hip_xent_backward_colsum": ([_vp, _vp, _vp, _vp, _f, _sz, _sz, _vp, _vp], _i),
     "vc_hip_profile_enable": ([_i], _i),
     "vc_hip_profile_labels": ([ctypes.c_char_p], _i),
     "vc_hip_profile_reset": ([], _i),

@@ -21,11 +21,11 @@ bool grad_enabled() { return t_grad_enabled; }
 namespace detail {
 
 namespace {
-thread_local ReluMaskOffer* t_relu_mask_offer = nullptr;
+thread_local GradientOffer* t_gradient_offer = nullptr;
 }
 
-ReluMaskOffer* relu_mask_offer() { return t_relu_mask_offer; }
-void set_relu_mask_offer(ReluMaskOffer* offer) { t_relu_mask_offer = offer; }
+GradientOffer* gradient_offer() { return t_gradient_offer; }
+void set_gradient_offer(GradientOffer* offer) { t_gradient_offer = offer; }
 
 SavedTensor::SavedTensor(const Tensor& value) : tensor_(value.detach()), version_(value.version()) {}
 

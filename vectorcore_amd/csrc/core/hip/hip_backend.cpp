@@ -136,6 +136,23 @@ public:
         mirror_ = m;
     }
 
+    // Column sums of this storage's contents as [rows, cols], computed by the
+    // kernel that wrote it (a bias gradient). Kept until taken or until the
+    // storage is written in place.
+    void set_column_sum(std::shared_ptr<HipStorage> sums, std::size_t rows, std::size_t cols) {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        column_sum_ = std::move(sums);
+        column_sum_rows_ = rows;
+        column_sum_cols_ = cols;
+    }
+    // The column sums for a [rows, cols] view of the whole storage, once.
+    std::shared_ptr<HipStorage> take_column_sum(std::size_t rows, std::size_t cols) const {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        if (!column_sum_ || rows != column_sum_rows_ || cols != column_sum_cols_ || rows * cols != elements_)
+            return nullptr;
+        return std::move(column_sum_);
+    }
+
     // The deferred product this storage still has to compute, if any (a copy
     // for building a product with a longer epilogue).
     std::optional<DeferredProduct> pending() const {
@@ -164,6 +181,7 @@ public:
         std::lock_guard<std::recursive_mutex> lock(state_mutex());
         (void)ptr();
         shadow_valid_ = false;
+        column_sum_.reset();  // about to be stale
         if (mirror_) {  // the published value is about to be stale
             (void)vc_hip_mirror_release(mirror_);
             mirror_ = nullptr;
@@ -205,6 +223,8 @@ private:
     mutable std::unique_ptr<DeferredProduct> deferred_;
     std::vector<std::weak_ptr<HipStorage>> readers_;
     vc_hip_mirror* mirror_ = nullptr;  // published value of a one-element result
+    mutable std::shared_ptr<HipStorage> column_sum_;  // see set_column_sum
+    std::size_t column_sum_rows_ = 0, column_sum_cols_ = 0;
     bool shadow_valid_;
 };
 
@@ -351,7 +371,7 @@ std::shared_ptr<Storage> HipBackend::matmul_relu_mask(const Storage& a, std::siz
                                                       const std::vector<std::size_t>& a_offsets,
                                                       const std::vector<std::size_t>& b_offsets, bool trans_a,
                                                       bool trans_b, const Storage& mask,
-                                                      std::size_t mask_offset) {
+                                                      std::size_t mask_offset, bool column_sum) {
     require(*this);
     if (a_offsets.size() != b_offsets.size() || a_offsets.empty())
         throw std::invalid_argument("HIP matmul needs one A and B offset per batch");
@@ -360,6 +380,14 @@ std::shared_ptr<Storage> HipBackend::matmul_relu_mask(const Storage& a, std::siz
     if (batch * m * n == 0) return out;
     if (k == 0) {  // empty inner dimension: the product, masked or not, is +0
         check(vc_hip_fill(out->ptr(), batch * m * n, 0.0F), "HIP fill failed");
+        return out;
+    }
+    if (column_sum && batch == 1 && a_offsets[0] == 0 && b_offsets[0] == 0) {
+        auto sums = fresh(n);
+        check(vc_hip_matmul_relu_mask_colsum(dptr(a, a_offset), dptr(b, b_offset), out->ptr(), m, k, n, trans_a ? 1 : 0,
+                                             trans_b ? 1 : 0, dptr(mask, mask_offset), sums->ptr()),
+              "HIP matmul failed");
+        out->set_column_sum(std::move(sums), m, n);
         return out;
     }
     check(vc_hip_matmul_relu_mask(dptr(a, a_offset), dptr(b, b_offset), out->ptr(), m, k, n, a_offsets.data(),
@@ -408,6 +436,10 @@ std::shared_ptr<Storage> HipBackend::reduce_axis(const Storage& input, std::size
     require(*this);
     if (length == 0 && operation != cpu::ReduceOp::Sum)
         throw std::invalid_argument("max/argmax over an empty axis is undefined");
+    if (operation == cpu::ReduceOp::Sum && outer == 1 && offset == 0) {
+        // Column sums the kernel that wrote the input already produced.
+        if (auto sums = as_hip(input).take_column_sum(length, inner)) return sums;
+    }
     auto out = fresh(outer * inner);
     if (outer * inner == 0) return out;
     check(vc_hip_reduce_axis(outer * length * inner != 0 ? dptr(input, offset) : nullptr, out->ptr(), outer, length, inner,
@@ -636,12 +668,21 @@ std::pair<std::shared_ptr<Storage>, std::shared_ptr<Storage>> HipBackend::cross_
 std::shared_ptr<Storage> HipBackend::cross_entropy_backward(const Storage& logits, std::size_t logits_offset,
                                                             const Storage& targets, const Storage& row_stats,
                                                             const Storage& grad_loss, std::size_t grad_offset,
-                                                            std::size_t rows, std::size_t classes) {
+                                                            std::size_t rows, std::size_t classes, bool column_sum) {
     require(*this);
     auto out = fresh(rows * classes);
     const auto* t = reinterpret_cast<const std::int32_t*>(as_hip(targets).ptr());
     // backward()'s seed is a host-known scalar: pass its value, no upload.
     const std::optional<float> seed = grad_offset == 0 ? hip_host_scalar(grad_loss) : std::nullopt;
+    if (column_sum && classes > 0) {
+        auto sums = fresh(classes);
+        check(vc_hip_xent_backward_colsum(dptr(logits, logits_offset), t, as_hip(row_stats).ptr(),
+                                          seed ? nullptr : dptr(grad_loss, grad_offset), seed ? *seed : 0.0F, rows,
+                                          classes, out->ptr(), sums->ptr()),
+              "HIP cross-entropy backward failed");
+        out->set_column_sum(std::move(sums), rows, classes);
+        return out;
+    }
     const int status =
         seed ? vc_hip_xent_backward_value(dptr(logits, logits_offset), t, as_hip(row_stats).ptr(), *seed, rows, classes,
                                           out->ptr())

@@ -20,22 +20,34 @@ struct GradFn {
     // Set by relu(): a tensor whose positive entries are those of the ReLU's
     // input (the input's version is checked). Lets the engine offer the ReLU
     // mask to the node that produces this node's upstream gradient (see
-    // ReluMaskOffer).
+    // GradientOffer).
     std::function<Tensor()> relu_mask;
+    // Set by add() when one operand is a row bias ([n] or [1, n]) added to a
+    // 2-D [m, n] operand: its index. The bias's gradient is then the column
+    // sum of this node's upstream gradient (sum_to_shape).
+    int row_bias_operand = -1;
 };
 
-// The engine's offer to the backward rule it is about to run: parent 0 of
-// that node is a ReLU output with no other consumer in the graph and no
-// retained gradient, so the rule may return parent 0's gradient already
-// multiplied by [relu_mask() > 0] (the ReLU rule's own arithmetic) and set
-// `taken`; the engine then passes that gradient through the ReLU node as is.
-struct ReluMaskOffer {
+// The engine's offer to the backward rule it is about to run, about the
+// gradient the rule returns for its parent 0. Either part may be absent.
+// - relu_mask: parent 0 is a ReLU output with no other consumer in the graph
+//   and no retained gradient, so the rule may return parent 0's gradient
+//   already multiplied by [relu_mask() > 0] (the ReLU rule's own arithmetic)
+//   and set `taken`; the engine then passes that gradient through the ReLU
+//   node as is.
+// - column_sum_wanted: the gradient the rule returns for parent 0 will reach a
+//   row-bias add (row_bias_operand) with no other consumer whose bias needs a
+//   gradient, unchanged (parent 0 is that add, or the ReLU above it whose mask
+//   is offered): the add's rule will take its column sum. A rule that can
+//   produce the sum on the way may leave it with the gradient's storage.
+struct GradientOffer {
     std::function<Tensor()> relu_mask;
+    bool column_sum_wanted = false;
     bool taken = false;
 };
 // The offer in effect on this thread, or null.
-ReluMaskOffer* relu_mask_offer();
-void set_relu_mask_offer(ReluMaskOffer* offer);
+GradientOffer* gradient_offer();
+void set_gradient_offer(GradientOffer* offer);
 
 struct TensorImpl {
     std::shared_ptr<Storage> storage;

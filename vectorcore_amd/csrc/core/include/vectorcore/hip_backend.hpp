@@ -49,13 +49,15 @@ public:
                                                   bool trans_b);
     // matmul() followed by the ReLU backward rule in the same kernel: the output
     // is multiplied by [mask > 0] (mask: the ReLU's input or output, laid out
-    // like the product).
+    // like the product). column_sum (one product only): the kernel also
+    // produces the output's column sums, which stay with the output storage
+    // until reduce_axis asks for exactly that sum (or the storage is written).
     [[nodiscard]] std::shared_ptr<Storage> matmul_relu_mask(const Storage& a, std::size_t a_offset, const Storage& b,
                                                             std::size_t b_offset, std::size_t m, std::size_t k,
                                                             std::size_t n, const std::vector<std::size_t>& a_offsets,
                                                             const std::vector<std::size_t>& b_offsets, bool trans_a,
                                                             bool trans_b, const Storage& mask,
-                                                            std::size_t mask_offset);
+                                                            std::size_t mask_offset, bool column_sum = false);
     [[nodiscard]] std::shared_ptr<Storage> transpose_last2(const Storage& input, std::size_t offset, std::size_t batch,
                                                            std::size_t rows, std::size_t cols);
     [[nodiscard]] std::shared_ptr<Storage> reduce_sum(const Storage& input, std::size_t offset, std::size_t count);
@@ -132,10 +134,13 @@ public:
     std::pair<std::shared_ptr<Storage>, std::shared_ptr<Storage>> cross_entropy_forward(
         const Storage& logits, std::size_t logits_offset, const Storage& targets, std::size_t rows,
         std::size_t classes);
+    // column_sum: the kernel also produces the gradient's column sums, kept
+    // with the returned storage for reduce_axis (as matmul_relu_mask does).
     [[nodiscard]] std::shared_ptr<Storage> cross_entropy_backward(const Storage& logits, std::size_t logits_offset,
                                                                   const Storage& targets, const Storage& row_stats,
                                                                   const Storage& grad_loss, std::size_t grad_offset,
-                                                                  std::size_t rows, std::size_t classes);
+                                                                  std::size_t rows, std::size_t classes,
+                                                                  bool column_sum = false);
 };
 
 // Host-side value of a one-element hip storage created from host data, if it

@@ -58,9 +58,13 @@ Tensor cross_entropy_hip(const Tensor& logits, const std::vector<std::size_t>& t
     std::shared_ptr<Storage> row_stats = std::move(stats);
     detail::attach_grad_fn(loss, {logits}, [saved, dev_targets, row_stats, rows, classes](const Tensor& g) {
         const Tensor x = saved.unpack();
+        // When the logits are h @ W + b, the backward kernel also leaves the
+        // column sums that b's add rule takes next (see GradientOffer).
+        const detail::GradientOffer* offer = detail::gradient_offer();
+        const bool column_sum = offer && offer->column_sum_wanted && !offer->relu_mask;
         auto d = HipBackend::instance().cross_entropy_backward(*x.impl()->storage, x.impl()->offset, *dev_targets,
                                                                *row_stats, *g.impl()->storage, g.impl()->offset, rows,
-                                                               classes);
+                                                               classes, column_sum);
         return std::vector<Tensor>{detail::make_tensor(std::move(d), {rows, classes}, false)};
     });
     return loss;

@@ -188,12 +188,13 @@ MatmulPlan plan_matmul(const Tensor& a, const Tensor& b, bool trans_a, bool tran
 
 // op(A) @ op(B) without a gradient rule (transposes read in place).
 Tensor matmul_kernel(const Tensor& a, const Tensor& b, bool trans_a, bool trans_b,
-                     const Tensor* relu_mask = nullptr) {
+                     const Tensor* relu_mask = nullptr, bool column_sum = false) {
     require_same_device(a, b);
     const MatmulPlan p = plan_matmul(a, b, trans_a, trans_b);
     if (relu_mask) {  // hip only: the product times [relu_mask > 0], relu_mask shaped like the product
         auto s = hip().matmul_relu_mask(st(a), off(a), st(b), off(b), p.m, p.k, p.n, p.a_offsets, p.b_offsets,
-                                        trans_a, trans_b, st(*relu_mask), off(*relu_mask));
+                                        trans_a, trans_b, st(*relu_mask), off(*relu_mask),
+                                        column_sum && p.batch == 1);
         Shape out_shape = p.out_batch;
         out_shape.push_back(p.m);
         out_shape.push_back(p.n);
@@ -259,6 +260,13 @@ Tensor add(const Tensor& a, const Tensor& b) {
     detail::attach_grad_fn(out, {a, b}, [=](const Tensor& g) {
         return two_grads(na ? detail::sum_to_shape(g, as) : Tensor(), nb ? detail::sum_to_shape(g, bs) : Tensor());
     });
+    if (out.impl()->grad_fn) {  // a row bias added to a matrix: its gradient is a column sum
+        const auto row_bias = [](const Shape& matrix, const Shape& bias) {
+            return matrix.size() == 2 && (bias == Shape{matrix[1]} || bias == Shape{1, matrix[1]});
+        };
+        if (row_bias(as, bs)) out.impl()->grad_fn->row_bias_operand = 1;
+        else if (row_bias(bs, as)) out.impl()->grad_fn->row_bias_operand = 0;
+    }
     return out;
 }
 
@@ -356,19 +364,21 @@ Tensor matmul(const Tensor& a, const Tensor& b) {
             } else if (na) {
                 // The engine may offer A's ReLU mask (A = relu(x) feeding only
                 // this product): dA * [x > 0] comes out of the same kernel.
-                detail::ReluMaskOffer* offer = detail::relu_mask_offer();
+                detail::GradientOffer* offer = detail::gradient_offer();
                 Shape product = p.out_batch;
                 product.push_back(p.m);
                 product.push_back(p.k);
                 std::optional<Tensor> relu_mask;
-                if (offer && product == as) {
+                if (offer && offer->relu_mask && product == as) {
                     relu_mask = offer->relu_mask();
                     if (relu_mask->device() != Device::hip() || relu_mask->shape() != as ||
                         relu_mask->strides() != contiguous_strides(as))
                         relu_mask.reset();
                 }
                 if (relu_mask) {
-                    grads[0] = matmul_kernel(g, bv, false, true, &*relu_mask);
+                    // When the ReLU's input is a bias add, the product's epilogue
+                    // also leaves the column sums that the add rule will ask for.
+                    grads[0] = matmul_kernel(g, bv, false, true, &*relu_mask, offer->column_sum_wanted);
                     offer->taken = true;
                 } else {
                     grads[0] = detail::sum_to_shape(matmul_kernel(g, bv, false, true), as);

@@ -310,21 +310,27 @@ void Tensor::backward(const Tensor& gradient) const {
             // node alone and is not kept: the rule may fuse it into its kernel
             // (hip products do). The gradient is the same either way.
             const auto& first = node->grad_fn->parents.empty() ? nullptr : node->grad_fn->parents[0];
-            detail::ReluMaskOffer offer;
-            const bool offered = first && upstream.device() == Device::hip() && first->grad_fn &&
-                                 first->grad_fn->relu_mask && first->requires_grad && !first->leaf &&
-                                 !first->retains_grad && consumers[first.get()] == 1;
-            if (offered) {
-                offer.relu_mask = first->grad_fn->relu_mask;
-                detail::set_relu_mask_offer(&offer);
-            }
+            detail::GradientOffer offer;
+            const bool on_hip = upstream.device() == Device::hip();
+            const bool offered = first && on_hip && first->grad_fn && first->grad_fn->relu_mask &&
+                                 first->requires_grad && !first->leaf && !first->retains_grad &&
+                                 consumers[first.get()] == 1;
+            if (offered) offer.relu_mask = first->grad_fn->relu_mask;
+            // Will parent 0's gradient reach a row-bias add unchanged (that add
+            // is parent 0, or the input of the ReLU whose mask is offered), the
+            // add consumed by nothing else and its bias needing a gradient?
+            const auto& add = offered ? (first->grad_fn->parents.empty() ? nullptr : first->grad_fn->parents[0]) : first;
+            const int bias = on_hip && add && add->grad_fn ? add->grad_fn->row_bias_operand : -1;
+            offer.column_sum_wanted = bias >= 0 && !add->leaf && !add->retains_grad && consumers[add.get()] == 1 &&
+                                      add->grad_fn->parents[static_cast<std::size_t>(bias)]->requires_grad;
+            if (offered || offer.column_sum_wanted) detail::set_gradient_offer(&offer);
             try {
                 grads = node->grad_fn->backward(upstream);
             } catch (...) {
-                detail::set_relu_mask_offer(nullptr);
+                detail::set_gradient_offer(nullptr);
                 throw;
             }
-            detail::set_relu_mask_offer(nullptr);
+            detail::set_gradient_offer(nullptr);
             if (offered && offer.taken) premasked.insert(first.get());
         }
         if (grads.size() != node->grad_fn->parents.size())

@@ -28,11 +28,13 @@
 // Tile order: workgroups are dispatched round-robin over the 8 XCDs, each with
 // its own L2. Consecutive tile ids are remapped onto one XCD and walked in
 // groups of 8 tile-rows, so tiles sharing A rows or B columns share an L2.
+#include "reduce_common.hpp"
 #include "vc_hip_internal.hpp"
 
 #include <algorithm>
 #include <limits>
 #include <optional>
+#include <string>
 #include <vector>
 
 namespace vchip {
@@ -72,6 +74,8 @@ struct GemmArgs {
     const float* relu_mask;        // null, or [batch][M][N]: C *= [relu_mask > 0] (fused ReLU backward)
     const float* bias;             // null, or [N]: C += bias[column] (fused row-bias add)
     int relu;                      // nonzero: C = C > 0 ? C : 0 after the bias (fused ReLU forward)
+    double* col_part;              // null, or [2 * (M / 128)][N] (batch 1, no split): column sums of the
+                                   //   final C values of each 64 rows of a full tile, in double
 };
 
 // The forward epilogue, in the order of the unfused ops: the row-broadcast add
@@ -406,6 +410,32 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
                         acc[i][j][v] = bias_relu(value, bias[j], p.relu != 0);
                     }
         }
+        if (p.col_part && row_lim >= BM) {
+            // Column sums of a full tile's final values, in double, one partial
+            // row per wave row (64 rows): each lane adds its 32 rows of a
+            // column (i, then v), then the two half-waves (rows 4 apart) are
+            // joined. Partial row 2 tm + wm / 64. The rows of a last, partial
+            // tile are summed from C by column_partials_kernel instead, so no
+            // row needs a bounds check here.
+            const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.col_part + (int64_t(2 * tm) + (wm >> 6)) * p.N + n0);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                double sum = 0.0;
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const float value = acc[i][j][v];
+                        sum += double(value);
+                    }
+                sum += __shfl_xor(sum, 32, 64);
+                const int col = wn + 32 * j + (lane & 31);
+                const uint64_t bits = __builtin_bit_cast(uint64_t, sum);
+                const uint32_t off = lane < 32 && col < col_lim ? uint32_t(col) * 8u : kOutOfRange;
+                __builtin_amdgcn_raw_buffer_store_b32(uint32_t(bits), rp, off, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(uint32_t(bits >> 32), rp, off + 4u, 0, 0);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -528,9 +558,11 @@ const char* variant_label(bool ta, bool tb) {
 void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t a_bstride,
           int64_t b_bstride, const std::vector<int64_t>* offsets, int64_t reduce, int64_t a_rstride, int64_t b_rstride,
           bool ta, bool tb, const float* relu_mask = nullptr, const float* bias = nullptr, bool relu = false,
-          bool in_caller_scope = false) {
+          bool in_caller_scope = false, float* column_sum = nullptr) {
     Device& d = require_device();
     if (M < 0 || N < 0 || K < 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "negative matrix dimension");
+    if (column_sum && (batch != 1 || reduce != 1))
+        fail(VC_HIP_ERR_INVALID_ARGUMENT, "a fused column sum needs a single product");
     if (M == 0 || N == 0 || batch == 0) return;
     if (!a || !b || !c) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul: null buffer");
     const bool force_simple = d.simple_gemm.load();  // the kernel in force for this call
@@ -635,6 +667,13 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     args.relu_mask = relu_mask;
     args.bias = bias;
     args.relu = relu ? 1 : 0;
+    // The column sum of C (a bias gradient) comes from the epilogue's per-tile
+    // partials when one MFMA launch writes C; otherwise it is a separate
+    // axis reduction of C afterwards.
+    const bool epilogue_sums = column_sum && !simple && splits == 1;
+    const int64_t full_tiles = M / BM;
+    Scratch col_part(epilogue_sums && full_tiles ? size_t(2 * full_tiles) * size_t(N) * sizeof(double) : 8);
+    if (epilogue_sums) args.col_part = col_part.as<double>();
     const double bytes =
         4.0 * (double(M * K + K * N) * double(reduce) + double(M * N) * (relu_mask ? 2.0 : 1.0)) * double(batch) +
         (bias ? 4.0 * double(N) : 0.0);
@@ -653,6 +692,18 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     }
     after_launch(label);
     if (prof) prof->done();
+    if (epilogue_sums) {
+        Profiled pc("column_sum_combine", 0.0,
+                    8.0 * double(2 * full_tiles) * double(N) + 4.0 * double(M - full_tiles * BM + 1) * double(N));
+        launch(red::column_partials_kernel, dim3(unsigned((N + 63) / 64)), dim3(64 * red::kCombineWaves), 0, d.stream,
+               col_part.as<double>(),
+               2 * full_tiles, static_cast<const float*>(c), full_tiles * BM, M, N, column_sum);
+        after_launch("column_sum_combine");
+        pc.done();
+    } else if (column_sum) {
+        const int rc = vc_hip_reduce_axis(c, column_sum, 1, size_t(M), size_t(N), VC_REDUCE_SUM);
+        if (rc != VC_HIP_OK) fail(rc, std::string("column sum of a product: ") + vc_hip_last_error());
+    }
 }
 
 // Per-batch offsets as the reference passes them: affine ones (the common
@@ -698,6 +749,22 @@ int vc_hip_matmul_relu_mask(const float* a, const float* b, float* c, size_t m, 
     return guard([&] {
         if (!mask) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask: null mask");
         matmul_offsets(a, b, c, m, k, n, a_offsets, b_offsets, batch, trans_a, trans_b, mask);
+    });
+}
+
+int vc_hip_matmul_relu_mask_colsum(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                                   int trans_a, int trans_b, const float* mask, float* column_sum) {
+    return guard([&] {
+        if (!mask || !column_sum) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask_colsum: null mask or column sum");
+        if (n == 0) return;
+        if (m == 0) {  // an empty column sum is zero
+            const int rc = vc_hip_fill(column_sum, n, 0.0f);
+            if (rc != VC_HIP_OK) fail(rc, vc_hip_last_error());
+            return;
+        }
+        if (k == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask_colsum needs k > 0");
+        gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), 1, 0, 0, nullptr, 1, 0, 0, trans_a != 0, trans_b != 0, mask,
+             nullptr, false, false, column_sum);
     });
 }
 

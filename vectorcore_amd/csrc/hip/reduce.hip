@@ -162,17 +162,21 @@ __global__ __launch_bounds__(kBlock) void cols_kernel(const float* __restrict__ 
 // ---- tiled column sums (few outputs, long axis: bias gradients) -------------------
 // Block (chunk, outer o, segment s): 16 column lanes x 16 row lanes. Column
 // lane c owns 4 adjacent columns (Vec) or 1; row lane r walks rows
-// a0 + r, a0 + r + 16, ... of the segment. Row lanes are then summed through
-// LDS in a fixed tree and one partial per (segment, column) is written.
-constexpr int kColLanes = 16, kRowLanes = 16;
+// a0 + r, a0 + r + 16, ... of the segment, sixteen rows in flight. A wave
+// holds four row lanes of the same columns (lanes c, c + 16, c + 32, c + 48):
+// they are joined with two exchanges (lane ^ 16, then lane ^ 32), then the
+// four waves in wave order through LDS. One partial per (segment, column).
+constexpr int kColLanes = 16, kRowLanes = 16, kColInFlight = 16;
 
 template <bool Vec>
 __global__ __launch_bounds__(kBlock) void colsum_tile_kernel(const float* __restrict__ x, double* __restrict__ part,
                                                              int64_t outer, int64_t len, int64_t inner, int64_t seg_len,
                                                              int64_t chunks) {
     constexpr int W = Vec ? 4 : 1;
-    __shared__ double lds[kRowLanes][kColLanes * W + 1];
+    constexpr int kWaves = kBlock / kWave;
+    __shared__ double lds[kWaves][kColLanes * W];
     const int c = threadIdx.x % kColLanes, rl = threadIdx.x / kColLanes;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int64_t chunk = blockIdx.x % chunks, o = blockIdx.x / chunks;
     const int64_t s = blockIdx.y;
     const int64_t col = (chunk * kColLanes + c) * W;
@@ -183,21 +187,21 @@ __global__ __launch_bounds__(kBlock) void colsum_tile_kernel(const float* __rest
     if (col < inner) {
         const float* base = x + o * len * inner + col;
         int64_t a = a0 + rl;
-        for (; a + 7 * kRowLanes < a1; a += 8 * kRowLanes) {  // eight rows in flight
+        for (; a + (kColInFlight - 1) * kRowLanes < a1; a += kColInFlight * kRowLanes) {
             if constexpr (Vec) {
-                f4 v[8];
+                f4 v[kColInFlight];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) v[u] = ld4(base + (a + u * kRowLanes) * inner);
+                for (int u = 0; u < kColInFlight; ++u) v[u] = ld4(base + (a + u * kRowLanes) * inner);
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
+                for (int u = 0; u < kColInFlight; ++u) {
                     acc[0] += double(v[u].x); acc[1] += double(v[u].y); acc[2] += double(v[u].z); acc[3] += double(v[u].w);
                 }
             } else {
-                float v[8];
+                float v[kColInFlight];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) v[u] = base[(a + u * kRowLanes) * inner];
+                for (int u = 0; u < kColInFlight; ++u) v[u] = base[(a + u * kRowLanes) * inner];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) acc[0] += double(v[u]);
+                for (int u = 0; u < kColInFlight; ++u) acc[0] += double(v[u]);
             }
         }
         for (; a < a1; a += kRowLanes) {
@@ -210,20 +214,23 @@ __global__ __launch_bounds__(kBlock) void colsum_tile_kernel(const float* __rest
         }
     }
 #pragma unroll
-    for (int w = 0; w < W; ++w) lds[rl][c * W + w] = acc[w];
-    __syncthreads();
-    // Fixed tree over the 16 row lanes: 8, 4, 2, 1.
-    for (int half = kRowLanes / 2; half > 0; half >>= 1) {
-        if (rl < half) {
-#pragma unroll
-            for (int w = 0; w < W; ++w) lds[rl][c * W + w] += lds[rl + half][c * W + w];
-        }
-        __syncthreads();
+    for (int w = 0; w < W; ++w) {
+        acc[w] += __shfl_xor(acc[w], 16, kWave);
+        acc[w] += __shfl_xor(acc[w], 32, kWave);
     }
-    if (rl == 0) {
+    if (lane < kColLanes) {
 #pragma unroll
-        for (int w = 0; w < W; ++w)
-            if (col + w < inner) part[(s * outer + o) * inner + col + w] = lds[0][c * W + w];
+        for (int w = 0; w < W; ++w) lds[wave][c * W + w] = acc[w];
+    }
+    __syncthreads();
+    if (wave == 0 && lane < kColLanes) {
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            double total = lds[0][c * W + w];
+#pragma unroll
+            for (int k = 1; k < kWaves; ++k) total += lds[k][c * W + w];
+            if (col + w < inner) part[(s * outer + o) * inner + col + w] = total;
+        }
     }
 }
 
@@ -320,8 +327,9 @@ void check_i32(int64_t v, const char* what) {
     if (v > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, std::string(what) + " exceeds the int32 index range");
 }
 
-// Segments of a column sum: a function of the shape only; aim at ~2048
-// workgroups, at least 64 rows per segment, at most 64 segments.
+// Segments of a column sum: a function of the shape only; aim at ~512
+// long-running workgroups (two per CU), at least 128 rows per segment, at
+// most 64 segments.
 struct ColumnPlan {
     bool vec;
     int64_t chunks, segs, seg_len;
@@ -334,8 +342,8 @@ ColumnPlan column_plan(const float* in, int64_t outer, int64_t len, int64_t inne
     c.chunks = (inner + width - 1) / width;
     const int64_t blocks_x = outer * c.chunks;
     if (blocks_x > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, "reduction too large");
-    int64_t segs = std::max<int64_t>(1, (2048 + blocks_x - 1) / blocks_x);
-    segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / 64), int64_t(kMaxColSegs)});
+    int64_t segs = std::max<int64_t>(1, (512 + blocks_x - 1) / blocks_x);
+    segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / 128), int64_t(kMaxColSegs)});
     c.seg_len = (len + segs - 1) / segs;
     c.segs = (len + c.seg_len - 1) / c.seg_len;
     return c;
@@ -471,8 +479,8 @@ void reduce_axis(const float* in, float* out, int64_t outer, int64_t len, int64_
 // copy until the process ends. On the host, `scratch` names a stand-in, not
 // device memory: host code uses only the address that hipGetSymbolAddress
 // returns for the current device. A column sum keeps segs * outputs at most
-// 2048 * 64 + outputs (double partials), so 2 MiB holds the column sums of up
-// to 2^17 outputs: the bias gradient of a [8192, 4096] layer needs 1 MiB. A
+// 512 * 64 + outputs (double partials), so 2 MiB holds the column sums of up
+// to 2^17 outputs: the bias gradient of a [8192, 4096] layer needs 256 KiB. A
 // max/argmax split over a long axis with few outputs needs 8 bytes per
 // (segment, output); a shape that needs more than the array is rejected.
 constexpr size_t kNoAllocScratchBytes = size_t(2) << 20;

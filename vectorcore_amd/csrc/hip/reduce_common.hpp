@@ -211,5 +211,40 @@ __global__ __launch_bounds__(kBlock) void sum_final_kernel(const double* __restr
     if (threadIdx.x == 0) out[0] = finish(float(total));
 }
 
+// out[col] = float(column sum) from partial rows written by a producing
+// kernel (part, `rows` rows of n doubles) and, for rows r >= c_row0 of the
+// producer's output C that no partial covers, from C itself. A workgroup takes 64
+// columns with 16 waves; wave w sums, for its lane's column, the partial rows
+// t = w, w + 16, ... and then the C rows c_row0 + w, c_row0 + w + 16, ... in
+// double, and the 16 wave sums are added in wave order: a fixed order.
+constexpr int kCombineWaves = 16;
+static __global__ __launch_bounds__(64 * kCombineWaves) void column_partials_kernel(
+    const double* __restrict__ part, int64_t rows, const float* __restrict__ c, int64_t c_row0, int64_t m, int64_t n,
+    float* __restrict__ out) {
+    __shared__ double wave_sum[kCombineWaves][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t col = int64_t(blockIdx.x) * 64 + lane;
+    double acc = 0.0;
+    if (col < n) {
+        int64_t t = w;
+        for (; t + 7 * kCombineWaves < rows; t += 8 * kCombineWaves) {  // eight loads in flight
+            double v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = part[(t + u * kCombineWaves) * n + col];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; t < rows; t += kCombineWaves) acc += part[t * n + col];
+        for (int64_t r = c_row0 + w; r < m; r += kCombineWaves) acc += double(c[r * n + col]);
+    }
+    wave_sum[w][lane] = acc;
+    __syncthreads();
+    if (w == 0 && col < n) {
+        double total = wave_sum[0][lane];
+        for (int k = 1; k < kCombineWaves; ++k) total += wave_sum[k][lane];
+        out[col] = float(total);
+    }
+}
+
 }  // namespace red
 }  // namespace vchip

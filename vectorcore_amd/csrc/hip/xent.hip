@@ -318,6 +318,82 @@ __global__ __launch_bounds__(kBlock) void xent_backward_kernel(const float* __re
     }
 }
 
+// The backward above, also leaving the column sums of dx (the gradient of a
+// bias added to the logits): a workgroup takes kColRows consecutive rows,
+// wave w the rows w, w + 4, ... of them, each held in registers as in the
+// forward (NV float4 per lane, the next row loaded before the current one is
+// finished). Each lane adds its columns' values over its rows in double;
+// the four waves are joined in wave order through LDS into one partial row
+// per workgroup, which red::column_partials_kernel then adds up. dx has the
+// same bits as xent_backward_kernel's.
+constexpr int kColRows = 16;
+
+template <int NV>
+__global__ __launch_bounds__(kBlock) void xent_backward_colsum_kernel(const float* __restrict__ x,
+                                                                      const int* __restrict__ targets,
+                                                                      const float* __restrict__ stats,
+                                                                      const float* __restrict__ grad_loss,
+                                                                      float grad_value, int64_t rows, int64_t len,
+                                                                      float* __restrict__ dx, double* __restrict__ part) {
+    __shared__ double joined[kRowsPerBlock - 1][NV * kWave * 4];
+    const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+    const float c = (grad_loss ? grad_loss[0] : grad_value) / float(rows);
+    const float neg_c = -c;
+    double acc[NV][4];
+#pragma unroll
+    for (int u = 0; u < NV; ++u) acc[u][0] = acc[u][1] = acc[u][2] = acc[u][3] = 0.0;
+    const int64_t first = int64_t(blockIdx.x) * kColRows + w;
+    const int64_t last = std::min<int64_t>(rows, int64_t(blockIdx.x + 1) * kColRows);
+    if (first < last) {
+        f4 cur[NV], next[NV];
+        load_row(cur, x + first * len, len, lane);
+        for (int64_t r = first; r < last; r += kRowsPerBlock) {
+            if (r + kRowsPerBlock < last) load_row(next, x + (r + kRowsPerBlock) * len, len, lane);
+            const float m = stats[2 * r], s = stats[2 * r + 1];
+            const float scale = c / s;
+            const int t = targets[r];
+            float* out = dx + r * len;
+#pragma unroll
+            for (int u = 0; u < NV; ++u) {
+                const int a = lane * 4 + u * kWave * 4;
+                if (a < len) {
+                    f4 g;
+                    g.x = scale * row_exp(cur[u].x - m) + (a == t ? neg_c : -0.0f);
+                    g.y = scale * row_exp(cur[u].y - m) + (a + 1 == t ? neg_c : -0.0f);
+                    g.z = scale * row_exp(cur[u].z - m) + (a + 2 == t ? neg_c : -0.0f);
+                    g.w = scale * row_exp(cur[u].w - m) + (a + 3 == t ? neg_c : -0.0f);
+                    *reinterpret_cast<f4*>(out + a) = g;
+                    acc[u][0] += double(g.x);
+                    acc[u][1] += double(g.y);
+                    acc[u][2] += double(g.z);
+                    acc[u][3] += double(g.w);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < NV; ++u) cur[u] = next[u];
+        }
+    }
+    if (w > 0) {
+#pragma unroll
+        for (int u = 0; u < NV; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) joined[w - 1][u * kWave * 4 + lane * 4 + e] = acc[u][e];
+    }
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+        for (int u = 0; u < NV; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int a = lane * 4 + u * kWave * 4 + e;
+                double total = acc[u][e];
+#pragma unroll
+                for (int k = 0; k < kRowsPerBlock - 1; ++k) total += joined[k][u * kWave * 4 + lane * 4 + e];
+                if (a < len) part[int64_t(blockIdx.x) * len + a] = total;
+            }
+    }
+}
+
 void xent_backward(const float* logits, const int32_t* targets, const float* row_stats, const float* grad_loss,
                    float grad_value, size_t rows, size_t classes, float* grad_logits) {
     Device& d = require_device();
@@ -407,6 +483,47 @@ int vc_hip_xent_backward(const float* logits, const int32_t* targets, const floa
 int vc_hip_xent_backward_value(const float* logits, const int32_t* targets, const float* row_stats, float grad_loss,
                                size_t rows, size_t classes, float* grad_logits) {
     return guard([&] { xent_backward(logits, targets, row_stats, nullptr, grad_loss, rows, classes, grad_logits); });
+}
+
+int vc_hip_xent_backward_colsum(const float* logits, const int32_t* targets, const float* row_stats,
+                                const float* grad_loss, float grad_loss_value, size_t rows, size_t classes,
+                                float* grad_logits, float* column_sum) {
+    return guard([&] {
+        Device& d = require_device();
+        if (!column_sum) fail(VC_HIP_ERR_INVALID_ARGUMENT, "xent_backward_colsum: null column sum");
+        if (classes == 0) return;
+        if (classes > size_t(std::numeric_limits<int>::max())) fail(VC_HIP_ERR_OVERFLOW, "too many classes");
+        const int64_t R = int64_t(rows), C = int64_t(classes);
+        const int64_t nv = (C + kWave * 4 - 1) / (kWave * 4);
+        const bool fused = rows > 0 && C % 4 == 0 && nv <= 8 && aligned16(logits) && aligned16(grad_logits);
+        if (!fused) {  // the plain backward, then a separate reduction of dx
+            xent_backward(logits, targets, row_stats, grad_loss, grad_loss_value, rows, classes, grad_logits);
+            const int rc = vc_hip_reduce_axis(grad_logits, column_sum, 1, rows, classes, VC_REDUCE_SUM);
+            if (rc != VC_HIP_OK) fail(rc, std::string("column sum of the cross-entropy gradient: ") + vc_hip_last_error());
+            return;
+        }
+        const int64_t blocks = (R + kColRows - 1) / kColRows;
+        if (blocks > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, "too many rows");
+        Scratch part(size_t(blocks) * size_t(C) * sizeof(double));
+        {
+            Profiled p("xent_backward", 0.0, 8.0 * double(R * C) + 12.0 * double(R) + 8.0 * double(blocks * C));
+#define VC_XENT_BWD_COLSUM(NV)                                                                                    \
+    launch((xent_backward_colsum_kernel<NV>), dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, logits, targets, \
+           row_stats, grad_loss, grad_loss_value, R, C, grad_logits, part.as<double>())
+            if (nv <= 1) VC_XENT_BWD_COLSUM(1);
+            else if (nv <= 2) VC_XENT_BWD_COLSUM(2);
+            else if (nv <= 4) VC_XENT_BWD_COLSUM(4);
+            else VC_XENT_BWD_COLSUM(8);
+#undef VC_XENT_BWD_COLSUM
+            after_launch("xent_backward");
+            p.done();
+        }
+        Profiled pc("column_sum_combine", 0.0, 8.0 * double(blocks * C) + 4.0 * double(C));
+        launch(red::column_partials_kernel, dim3(unsigned((C + 63) / 64)), dim3(64 * red::kCombineWaves), 0, d.stream,
+               part.as<double>(), blocks, static_cast<const float*>(grad_logits), R, R, C, column_sum);
+        after_launch("column_sum_combine");
+        pc.done();
+    });
 }
 
 }  // extern "C"

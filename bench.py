@@ -11,9 +11,11 @@ buffers are recycled through the device pool.
 
 Prints one JSON line: whole-job train-steps/s, the backward-GEMM roofline
 (MFMA-bound; HIP events carried by the backward-GEMM dispatches on the library
-stream over the timed region, the only kernels timed there), the reduction
-bandwidth and forward-GEMM rate from a short breakdown pass that times every
-kernel, and the reference CPU path timed on this host on the same full-batch step.
+stream over the timed region, the only kernels timed there), the forward-GEMM
+rate and the bias-gradient sums from a short breakdown pass that times every
+kernel, the standalone reduction kernel on the step's bias-gradient shapes, the
+other configurations (--config runs one of them alone), and the reference CPU
+path timed on this host on the same full-batch step.
 vs_baseline stays null: no published figure exists for this metric (the
 reference publishes Apple M4 numbers at other shapes only).
 """
@@ -41,6 +43,15 @@ BREAKDOWN_STEPS = 5
 
 def log(*args):
     print(*args, file=sys.stderr, flush=True)
+
+
+def copy_calibration_pass(vc):
+    """A plain streaming pass of known size (read 256 MiB, write 256 MiB) whose
+    FETCH_SIZE/WRITE_SIZE counters calibrate rocprofv3's traffic readings."""
+    src = vc.Tensor.zeros([64 << 20], device="hip")
+    for _ in range(3):
+        _ = -src
+    vc.synchronize()
 
 
 def gpu_bench(steps: int, warmup: int, copy_calibration: bool = False):
@@ -72,13 +83,7 @@ def gpu_bench(steps: int, warmup: int, copy_calibration: bool = False):
         return loss.item()
 
     if copy_calibration:
-        # A plain streaming pass of known size (read 256 MiB, write 256 MiB)
-        # whose FETCH_SIZE/WRITE_SIZE counters calibrate the traffic readings.
-        src = vc.Tensor.zeros([64 << 20], device="hip")
-        for _ in range(3):
-            _ = -src
-        vc.synchronize()
-        del src, _
+        copy_calibration_pass(vc)
     losses = [step() for _ in range(warmup)]
     allocs_before = vc.hip_pool_stats()["device_allocations"]
     # Timed region. Only the backward GEMMs carry HIP events (as dispatch
@@ -180,21 +185,15 @@ def _profiled(vc, fn, labels=None, repeats=5, setup=None):
             for k, v in out.items()}
 
 
-def config_measurements(cpu: bool):
-    """The reference's other configurations on the hip device: throughput, the
-    roofline fraction of their kernels, and the reference CPU path on the same
-    inputs (whole calls, including the harness's host copies), in this run."""
-    import numpy as np
+def _reference(cpu: bool):
+    if not cpu:
+        return None
+    from oracle import kernels as K
+    return K.Reference() if K.Reference.available() else None
 
-    import vectorcore_amd as vc
-    from vectorcore_amd import workloads as W
-    ref = None
-    if cpu:
-        from oracle import kernels as K
-        ref = K.Reference() if K.Reference.available() else None
-    out = {}
 
-    # Spiral classifier train step (launch-bound; no roofline).
+def measure_spiral(vc, W, ref):
+    """Spiral classifier train step (launch-bound; no roofline)."""
     sp = W.spiral()
     ps = []
     for w, b in zip(sp["weights"], sp["biases"]):
@@ -225,35 +224,38 @@ def config_measurements(cpu: bool):
         net = ref.mlp(sp["weights"], sp["biases"], sp["x"], sp["targets"])
         net.step(sp["lr"])
         c1["cpu_reference_steps_per_s"] = round(1e3 / _median_ms(lambda: net.step(sp["lr"]), 50), 1)
-    out["spiral_train_step"] = c1
+    return c1
 
-    # Batched matmul backward, dA = dC B^T (NT) and dB = A^T dC (TN).
+
+def measure_bmm(vc, W, ref, bkey):
+    """Batched matmul backward, dA = dC B^T (NT) and dB = A^T dC (TN)."""
     bm = W.bmm()
     flops = 2.0 * 8 * 1024 ** 3
-    for name, bkey in (("batched_matmul_backward", "b"), ("batched_matmul_backward_broadcast_b", "b_shared")):
-        a = vc.Tensor(bm["a"], requires_grad=True, device="hip")
-        b = vc.Tensor(bm[bkey], requires_grad=True, device="hip")
-        dc = vc.Tensor(bm["dc"], device="hip")
+    a = vc.Tensor(bm["a"], requires_grad=True, device="hip")
+    b = vc.Tensor(bm[bkey], requires_grad=True, device="hip")
+    dc = vc.Tensor(bm["dc"], device="hip")
 
-        def fwd_bwd():
-            (a @ b).backward(dc)
-            vc.zero_grad([a, b])
-            vc.synchronize()
+    def fwd_bwd():
+        (a @ b).backward(dc)
+        vc.zero_grad([a, b])
+        vc.synchronize()
 
-        fwd_bwd()
-        prof = _profiled(vc, fwd_bwd, labels=list(BWD_GEMM_LABELS))
-        ms = sum(v["ms"] for v in prof.values())
-        tflops = 2 * flops / ms / 1e9
-        c2 = {"workload": f"A [8,1024,1024] @ B {list(bm[bkey].shape)}, backward dA and dB",
-              "bound": "mfma", "bwd_gemm_tflops": round(tflops, 1), "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 3),
-              "bwd_gemm_ms": round(ms, 3), "hip_ms_forward_backward": round(_median_ms(fwd_bwd, 10), 3)}
-        if ref:
-            c2["cpu_reference_ms_forward_backward"] = round(
-                _median_ms(lambda: ref.matmul_backward(bm["a"], bm[bkey], bm["dc"]), 1), 1)
-        out[name] = c2
-        del a, b, dc
+    fwd_bwd()
+    prof = _profiled(vc, fwd_bwd, labels=list(BWD_GEMM_LABELS))
+    ms = sum(v["ms"] for v in prof.values())
+    tflops = 2 * flops / ms / 1e9
+    c2 = {"workload": f"A [8,1024,1024] @ B {list(bm[bkey].shape)}, backward dA and dB",
+          "bound": "mfma", "bwd_gemm_tflops": round(tflops, 1), "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 3),
+          "bwd_gemm_ms": round(ms, 3), "per_kernel_us": {k: round(v["ms"] * 1e3, 1) for k, v in prof.items()},
+          "hip_ms_forward_backward": round(_median_ms(fwd_bwd, 10), 3)}
+    if ref:
+        c2["cpu_reference_ms_forward_backward"] = round(
+            _median_ms(lambda: ref.matmul_backward(bm["a"], bm[bkey], bm["dc"]), 1), 1)
+    return c2
 
-    # Activation chain y = sigmoid(relu(x + bias)) * exp(0.1 x); backward for dx, dbias.
+
+def measure_activation(vc, W, ref):
+    """Activation chain y = sigmoid(relu(x + bias)) * exp(0.1 x); backward for dx, dbias."""
     ac = W.activation()
     x = vc.Tensor(ac["x"], requires_grad=True, device="hip")
     bias = vc.Tensor(ac["bias"], requires_grad=True, device="hip")
@@ -287,15 +289,18 @@ def config_measurements(cpu: bool):
           "bound": "hbm", "bwd_kernel_gbs": round(kbytes / kms / 1e6, 1),
           "frac": round(kbytes / kms / 1e6 / HBM_PEAK_GBS, 3), "bwd_kernels_ms": round(kms, 3),
           "bwd_kernel_launches": int(sum(v["launches"] for v in prof.values())),
+          "bwd_bytes_mb": round(kbytes / 1e6, 1),
           "min_bytes_rate_gbs": round(min_bytes / kms / 1e6, 1),
+          "per_label_us": {k: round(v["ms"] * 1e3, 1) for k, v in prof.items()},
           "hip_ms_forward_backward": round(_median_ms(fwd_bwd3, 10), 3)}
     if ref:
         c3["cpu_reference_ms_forward_backward"] = round(
             _median_ms(lambda: ref.activation_backward(ac["x"], ac["bias"], ac["dy"]), 1), 1)
-    out["activation_backward"] = c3
-    del x, bias, dy, holder
+    return c3
 
-    # Mean softmax cross-entropy forward + backward, argmax over classes.
+
+def measure_xent(vc, W, ref):
+    """Mean softmax cross-entropy forward + backward, argmax over classes."""
     xe = W.xent()
     lg = vc.Tensor(xe["logits"], requires_grad=True, device="hip")
     tg = xe["targets"]
@@ -318,7 +323,52 @@ def config_measurements(cpu: bool):
             c4[label] = {"ms": round(v["ms"], 4), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)}
     if ref:
         c4["cpu_reference_ms"] = round(_median_ms(lambda: ref.cross_entropy(xe["logits"], tg), 1), 1)
-    out["cross_entropy"] = c4
+    return c4
+
+
+def measure_column_sums(vc):
+    """The standalone column-sum reduction (axis-0 sum) on the train step's
+    bias-gradient shapes: the kernel a bias gradient takes when its producer
+    cannot keep the sums (inside the step they come from the producers)."""
+    import numpy as np
+    rng = np.random.default_rng(5)
+    out = {}
+    total_bytes = total_ms = 0.0
+    for rows, cols, times in ((BATCH, 4096, 2), (BATCH, 1000, 1)):
+        t = vc.Tensor(rng.standard_normal((rows, cols)).astype(np.float32), device="hip")
+        t.sum(0)
+        prof = _profiled(vc, lambda: t.sum(0), labels=["reduce_axis_sum"], repeats=10)["reduce_axis_sum"]
+        gbs = prof["bytes"] / prof["ms"] / 1e6
+        out[f"{rows}x{cols}"] = {"us": round(prof["ms"] * 1e3, 2), "gbs": round(gbs, 1),
+                                 "frac": round(gbs / HBM_PEAK_GBS, 3)}
+        total_bytes += times * prof["bytes"]
+        total_ms += times * prof["ms"]
+    out["step_shapes_gbs"] = round(total_bytes / total_ms / 1e6, 1)
+    return out
+
+
+CONFIGS = ("spiral_train_step", "batched_matmul_backward", "batched_matmul_backward_broadcast_b",
+           "activation_backward", "cross_entropy", "column_sums")
+
+
+def config_measurements(cpu: bool, only=None):
+    """The reference's other configurations on the hip device: throughput, the
+    roofline fraction of their kernels, and the reference CPU path on the same
+    inputs (whole calls, including the harness's host copies), in this run."""
+    import vectorcore_amd as vc
+    from vectorcore_amd import workloads as W
+    ref = _reference(cpu)
+    run = {
+        "spiral_train_step": lambda: measure_spiral(vc, W, ref),
+        "batched_matmul_backward": lambda: measure_bmm(vc, W, ref, "b"),
+        "batched_matmul_backward_broadcast_b": lambda: measure_bmm(vc, W, ref, "b_shared"),
+        "activation_backward": lambda: measure_activation(vc, W, ref),
+        "cross_entropy": lambda: measure_xent(vc, W, ref),
+        "column_sums": lambda: measure_column_sums(vc),
+    }
+    out = {}
+    for name in (only or CONFIGS):
+        out[name] = run[name]()
     if ref:
         out["cpu_reference_threads"] = ref.threads()
     return out
@@ -343,6 +393,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the other configurations' measurements")
+    ap.add_argument("--config", choices=CONFIGS,
+                    help="run only this configuration's measurement (no train-step bench) and print it as JSON")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first stream 256 MiB through a negate kernel (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -350,6 +402,14 @@ def main():
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the data-parallel sharding of "
               "this workload is a design note, not a launched path)", file=sys.stderr)
         sys.exit(2)
+
+    if args.config:
+        if args.copy_calibration:
+            import vectorcore_amd as vc
+            copy_calibration_pass(vc)
+        print(json.dumps({args.config: config_measurements(cpu=not args.no_cpu_baseline, only=[args.config])[args.config]}),
+              flush=True)
+        return
 
     r = gpu_bench(args.steps, args.warmup, args.copy_calibration)
     prof = r["prof"]
@@ -361,8 +421,7 @@ def main():
     bwd_tflops = bwd_flops / bwd_ms / 1e9 if bwd_ms else None
     # Per-kernel figures from the breakdown pass.
     bd, nb = r["breakdown"], r["breakdown_steps"]
-    red = bd.get("reduce_axis_sum", {})
-    reduce_gbs = red["bytes"] / red["ms"] / 1e6 if red.get("ms") else None
+    combine = bd.get("column_sum_combine", {})
     fwd = bd.get("gemm_nn", {})
     fwd_tflops = fwd["flops"] / fwd["ms"] / 1e9 if fwd.get("ms") else None
     device_ms = sum(v["ms"] for v in bd.values()) / nb
@@ -402,12 +461,17 @@ def main():
                    "global_batch": BATCH, "layers": list(DIMS), "parallelism": "single GPU"},
         "bwd_gemm_tflops": round(bwd_tflops, 2) if bwd_tflops else None,
         "fwd_gemm_tflops": round(fwd_tflops, 2) if fwd_tflops else None,
-        "reduce_gbs": round(reduce_gbs, 1) if reduce_gbs else None,
-        "reduce_hbm_frac": round(reduce_gbs / HBM_PEAK_GBS, 4) if reduce_gbs else None,
+        "bias_grad_sums": {
+            "how": "column sums kept by the producing kernels (masked NT product epilogue for db1 and db2, "
+                   "cross-entropy backward for db3), then one fixed-order combine pass each",
+            "combine_launches_per_step": round(combine.get("launches", 0) / nb, 2),
+            "combine_us_per_step": round(combine.get("ms", 0.0) * 1e3 / nb, 2),
+        },
         "device_ms_per_step": round(device_ms, 3),
         "timing": "value and roofline: the timed steps, with events on the backward GEMMs only; "
-                  "fwd_gemm_tflops, reduce_gbs, device_ms_per_step: a breakdown pass of "
-                  f"{r['breakdown_steps']} further steps with every kernel timed",
+                  "fwd_gemm_tflops, bias_grad_sums, device_ms_per_step: a breakdown pass of "
+                  f"{r['breakdown_steps']} further steps with every kernel timed; reduce_gbs: the standalone "
+                  "column-sum kernel on the step's bias-gradient shapes (configs.column_sums)",
         "pool_new_allocations_in_timed_steps": r["new_allocations"],
         "loss_first_last": [round(r["losses"][0], 5), round(r["losses"][-1], 5)],
         "device": r["device"],
@@ -422,6 +486,10 @@ def main():
         t0 = time.perf_counter()
         out["configs"] = config_measurements(cpu=not args.no_cpu_baseline)
         log(f"  other configurations took {time.perf_counter() - t0:.1f} s")
+        sums = out["configs"]["column_sums"]
+        # The reduction kernel on the step's bias-gradient shapes ([8192, 4096] twice, [8192, 1000]).
+        out["reduce_gbs"] = sums["step_shapes_gbs"]
+        out["reduce_hbm_frac"] = round(sums["step_shapes_gbs"] / HBM_PEAK_GBS, 4)
     print(json.dumps(out), flush=True)
 
 

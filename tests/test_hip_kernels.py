@@ -467,6 +467,18 @@ def test_cross_entropy_backward_with_the_seed_by_value_is_bitexact():
     assert C.lib().vc_hip_xent_backward(dl.ptr, dt.ptr, stats.ptr, None, rows, classes, by_ptr.ptr) != 0
 
 
+def test_cross_entropy_forward_back_to_back_calls():
+    # The register-held forward finishes the loss in whichever row block
+    # ends last and returns its block counter to zero: calls in a row, with
+    # grids of different sizes, each give the oracle's loss.
+    from oracle import autograd as A
+    for i, (rows, classes) in enumerate([(5000, 1000), (7, 1000), (300, 40), (5000, 1000), (64, 4096), (1, 8)] * 2):
+        xe = W.xent(rows=rows, classes=classes, seed=100 + i)
+        loss, _ = xent_dev(xe["logits"], xe["targets"])
+        want = A.cross_entropy(A.T(xe["logits"]), xe["targets"]).data
+        np.testing.assert_allclose(loss, want, rtol=1e-6, err_msg=f"call {i}: {rows}x{classes}")
+
+
 def test_cross_entropy_register_and_streaming_paths_agree():
     # Aligned rows of 1000 classes take the register-held forward and the
     # vector backward; the same rows one float off 16-byte alignment take the

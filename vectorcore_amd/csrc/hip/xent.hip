@@ -31,6 +31,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 constexpr unsigned kBlock = 256;
 constexpr int kRowsPerBlock = kBlock / kWave;
+constexpr int64_t kXentBlocksPerCu = 8;  // workgroups per CU of the register-held forward
 
 __device__ inline f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 
@@ -102,6 +103,17 @@ __device__ inline float wave_max(float v) {
     return o > v ? o : v;
 }
 
+// Smallest value over the wavefront (inputs never NaN).
+__device__ inline float wave_min(float v) {
+    const int lane = red::lane_id();
+    v = __builtin_fminf(v, red::partner<0>(v, lane));
+    v = __builtin_fminf(v, red::partner<1>(v, lane));
+    v = __builtin_fminf(v, red::partner<2>(v, lane));
+    v = __builtin_fminf(v, red::partner<3>(v, lane));
+    v = __builtin_fminf(v, red::partner<4>(v, lane));
+    return __builtin_fminf(v, red::partner<5>(v, lane));
+}
+
 // Row statistics and loss term of one row from values in registers (NV
 // float4 per lane; element a = 4 lane + 256 u + component, a multiple-of-4
 // row of at most 256 NV classes; elements past the row hold -inf). Each lane
@@ -112,15 +124,17 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
                                    float* __restrict__ stats) {
     // The reference's max is the first strict maximum, skipping NaN after
     // element 0. Its value is the largest non-NaN element, whichever index
-    // holds it, except for the sign of a zero maximum (the first zero wins)
-    // and a NaN element 0, both settled below.
-    float mx = -__builtin_inff();
+    // holds it (fmaxf ignores NaN too), except for the sign of a zero maximum
+    // (the first zero wins) and a NaN element 0, both settled below. The row
+    // minimum (padding left out) tells whether any element is -inf, whose
+    // shifted value is the one non-finite case the exp-sum does not show.
+    float mx = -__builtin_inff(), mn = __builtin_inff();
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
-        mx = v[u].x > mx ? v[u].x : mx;
-        mx = v[u].y > mx ? v[u].y : mx;
-        mx = v[u].z > mx ? v[u].z : mx;
-        mx = v[u].w > mx ? v[u].w : mx;
+        mx = __builtin_fmaxf(__builtin_fmaxf(mx, v[u].x), __builtin_fmaxf(__builtin_fmaxf(v[u].y, v[u].z), v[u].w));
+        const bool in_row = lane * 4 + u * kWave * 4 < len;  // a whole float4 of the row, or of padding
+        const float lo = __builtin_fminf(__builtin_fminf(v[u].x, v[u].y), __builtin_fminf(v[u].z, v[u].w));
+        mn = in_row ? __builtin_fminf(mn, lo) : mn;
     }
     mx = wave_max(mx);
     const float first = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v[0].x)));
@@ -146,20 +160,23 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
     // Elements past the row give exp(-inf - m) = 0 (or NaN when m is -inf or
     // NaN, and then every real element's term is NaN too): adding them leaves
     // the sum unchanged.
-    double acc = 0.0;
-    bool nonfinite = false;  // any shifted value in the row not finite, target included
+    // Four double chains per lane, one per float4 component, joined in
+    // component order: the streaming path adds in the same order.
+    double c0 = 0.0, c1 = 0.0, c2 = 0.0, c3 = 0.0;
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
-        const int a = lane * 4 + u * kWave * 4;
-        const float s0 = v[u].x - m, s1 = v[u].y - m, s2 = v[u].z - m, s3 = v[u].w - m;
-        acc += double(row_exp(s0));
-        acc += double(row_exp(s1));
-        acc += double(row_exp(s2));
-        acc += double(row_exp(s3));
-        nonfinite |= (a < len) & (!isfinite(s0) | !isfinite(s1) | !isfinite(s2) | !isfinite(s3));
+        c0 += double(row_exp(v[u].x - m));
+        c1 += double(row_exp(v[u].y - m));
+        c2 += double(row_exp(v[u].z - m));
+        c3 += double(row_exp(v[u].w - m));
     }
+    const double acc = red::wave_sum(((c0 + c1) + c2) + c3);
+    // Some shifted value is not finite exactly when m is not finite, an
+    // element is -inf, or the sum is NaN (a NaN or +inf element makes its own
+    // term, or every term, NaN).
+    const bool nonfinite = !isfinite(m) || !(wave_min(mn) > -__builtin_inff()) || acc != acc;
     int bad = 0;  // a non-target log-prob that is not finite
-    if (__ballot(nonfinite) != 0) {  // rare: decide exactly, leaving the target out
+    if (nonfinite) {  // rare: decide exactly, leaving the target out
 #pragma unroll
         for (int u = 0; u < NV; ++u) {
             const int a = lane * 4 + u * kWave * 4;
@@ -170,7 +187,6 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
             }
         }
     }
-    acc = red::wave_sum(acc);
     bad = red::wave_or(bad);
     // The target's logit from the registers of the lane holding it (t is
     // wave-uniform): element t is component t % 4 of v[t / 256] on lane
@@ -202,16 +218,45 @@ __device__ inline void load_row(f4 (&v)[NV], const float* __restrict__ row, int6
 // on the current one, so memory latency overlaps the exp work of the row
 // before. The loss terms are summed on the way: each wavefront in row order,
 // then the block's wavefronts in order, into one double per block.
+//
+// The block that finishes last also finishes the loss, so the forward is one
+// launch: each block writes its partial with a device-scope store, waits for
+// it to complete, then counts itself in on its group's device-scope counter
+// (groups of kDoneGroup blocks, one counter per 128-byte line, so the count
+// is not one long queue on one address); the block that completes a group
+// resets that counter and counts the group in on the top counter. The block
+// that completes the last group reads every partial with device-scope loads
+// and adds them as sum_final_kernel does (thread t takes blocks t, t + 256,
+// ..., then the fixed workgroup tree), so the loss does not depend on which
+// block is last, and resets the top counter for the next launch (launches on
+// the library's one stream never overlap).
+constexpr unsigned kDoneGroup = 64, kDoneGroups = 64, kDoneStride = 32;
+__device__ unsigned int g_xent_group_done[kDoneGroups * kDoneStride];
+__device__ unsigned int g_xent_groups_done;
+
+// loss = -(float)(sum of row terms) / (float)rows: negate, then divide, as
+// -(...).sum() / batch evaluates (src/nn.cpp:52).
+struct NegateDivide {
+    float rows;
+    __device__ float operator()(float sum) const {
+        const float negated = -sum;
+        return negated / rows;
+    }
+};
+
 template <int NV>
-__global__ __launch_bounds__(kBlock) void xent_rows_cached_kernel(const float* __restrict__ x,
+// Six waves per SIMD (at most 80 registers) fit without spilling and measured
+// 2-10% faster than the unconstrained allocation (4 waves); eight spill.
+__global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float* __restrict__ x,
                                                                   const int* __restrict__ targets, int64_t rows,
                                                                   int64_t len, float* __restrict__ stats,
-                                                                  double* __restrict__ part) {
+                                                                  double* __restrict__ part, float* __restrict__ loss) {
     __shared__ double wave_terms[kRowsPerBlock];
+    __shared__ int last_block;
     const int lane = threadIdx.x % kWave;
     const int64_t first = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
     const int64_t waves = int64_t(gridDim.x) * kRowsPerBlock;
-    double total = 0.0;  // lane 0: this wavefront's terms
+    double total = 0.0;  // lane 0: this wavefront's terms, in row order
     if (first < rows) {
         f4 cur[NV], next[NV];
         load_row(cur, x + first * len, len, lane);
@@ -234,7 +279,46 @@ __global__ __launch_bounds__(kBlock) void xent_rows_cached_kernel(const float* _
     if (threadIdx.x == 0) {
         double sum = wave_terms[0];
         for (int w = 1; w < kRowsPerBlock; ++w) sum += wave_terms[w];
-        part[blockIdx.x] = sum;
+        __hip_atomic_store(&part[blockIdx.x], sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // A device-scope store is acknowledged once it is visible at device
+        // scope; waiting for every outstanding memory operation (vmcnt 0)
+        // therefore orders it before the count below. (A release fence would
+        // also write back the whole L2, which this store does not need.)
+        __builtin_amdgcn_s_waitcnt(0);
+        const unsigned group = blockIdx.x / kDoneGroup, groups = (gridDim.x + kDoneGroup - 1) / kDoneGroup;
+        const unsigned members = min(kDoneGroup, gridDim.x - group * kDoneGroup);
+        unsigned* counter = &g_xent_group_done[group * kDoneStride];
+        bool last = false;
+        if (__hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == members) {
+            __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            last = __hip_atomic_fetch_add(&g_xent_groups_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
+                   groups;
+        }
+        last_block = last;
+    }
+    __syncthreads();
+    if (!last_block) return;
+    // Device-scope loads (cache policy sc1 = 16), eight in flight per thread,
+    // then added in block order.
+    const __amdgpu_buffer_rsrc_t rp =
+        __builtin_amdgcn_make_buffer_rsrc(part, short(0), int(gridDim.x * sizeof(double)), 0x00020000);
+    double acc = 0.0;
+    for (unsigned b0 = threadIdx.x; b0 < gridDim.x; b0 += 8 * blockDim.x) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const unsigned b = b0 + u * blockDim.x;  // past the grid: outside the descriptor, reads 0 (not added)
+            v[u] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rp, b * 8u, 0, 16));
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (b0 + u * blockDim.x < gridDim.x) acc += v[u];
+    }
+    const double sum = red::block_sum(acc, wave_terms);
+    if (threadIdx.x == 0) {
+        loss[0] = NegateDivide{float(rows)}(float(sum));
+        __hip_atomic_store(&g_xent_groups_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -252,17 +336,19 @@ __global__ __launch_bounds__(kBlock) void xent_rows_kernel(const float* __restri
     const float m = row_max(row, len, lane, Vec);
     double acc = 0.0;
     int bad = 0;  // a non-target log-prob that is not finite
-    if (Vec) {
+    if (Vec) {  // four component chains, joined in order, as the register-held path adds
+        double c0 = 0.0, c1 = 0.0, c2 = 0.0, c3 = 0.0;
         for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
             const f4 v = ld4(row + a);
             const float s0 = v.x - m, s1 = v.y - m, s2 = v.z - m, s3 = v.w - m;
-            acc += double(row_exp(s0));
-            acc += double(row_exp(s1));
-            acc += double(row_exp(s2));
-            acc += double(row_exp(s3));
+            c0 += double(row_exp(s0));
+            c1 += double(row_exp(s1));
+            c2 += double(row_exp(s2));
+            c3 += double(row_exp(s3));
             bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) | (a + 2 != t && !isfinite(s2)) |
                    (a + 3 != t && !isfinite(s3));
         }
+        acc = ((c0 + c1) + c2) + c3;
     } else {
         for (int64_t a = lane; a < len; a += kWave) {
             const float s = row[a] - m;
@@ -277,16 +363,6 @@ __global__ __launch_bounds__(kBlock) void xent_rows_kernel(const float* __restri
         terms[r] = write_row(r, len, t, in_row ? row[t] : 0.0f, m, acc, bad, stats);
     }
 }
-
-// loss = -(float)(sum of row terms) / (float)rows: negate, then divide, as
-// -(...).sum() / batch evaluates (src/nn.cpp:52).
-struct NegateDivide {
-    float rows;
-    __device__ float operator()(float sum) const {
-        const float negated = -sum;
-        return negated / rows;
-    }
-};
 
 template <bool Vec>
 __global__ __launch_bounds__(kBlock) void xent_backward_kernel(const float* __restrict__ x, const int* __restrict__ targets,
@@ -433,13 +509,13 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
         Profiled p("xent_forward", 0.0, 4.0 * double(R * C) + 4.0 * double(R) + 8.0 * double(R));
         // Rows of up to 4096 classes are held in registers (NV float4 per lane),
-        // with at most 8 workgroups per CU walking the rows (5 fit at once at
-        // this kernel's register use; sizing the grid to exactly one resident
-        // round measured the same).
+        // with at most 8 workgroups per CU walking the rows (6 fit at once at
+        // this kernel's register use; 3 to 12 per CU measured within 3%).
         const int64_t nv = vec ? (C + kWave * 4 - 1) / (kWave * 4) : 0;
-        const unsigned cached_grid = unsigned(std::min<int64_t>((R + kRowsPerBlock - 1) / kRowsPerBlock,
-                                                                int64_t(d.cu_count) * 8));
-        int64_t blocks = 0;  // loss partials, one double each
+        const unsigned cached_grid = unsigned(std::min<int64_t>(
+            {(R + kRowsPerBlock - 1) / kRowsPerBlock, int64_t(d.cu_count) * kXentBlocksPerCu,
+             int64_t(kDoneGroup) * kDoneGroups}));
+        int64_t blocks = 0;  // loss partials of the streaming path, one double each
         Scratch part(size_t(std::max<int64_t>(cached_grid, (R + red::sum_chunk(R) - 1) / red::sum_chunk(R))) *
                      sizeof(double));
         if (!vec || nv > 16) {
@@ -451,22 +527,22 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
             blocks = (R + chunk - 1) / chunk;
             launch(red::sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream,
                    terms.as<float>(), part.as<double>(), R, chunk);
+            after_launch("xent_forward");
+            launch(red::sum_final_kernel<NegateDivide>, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), loss,
+                   blocks, NegateDivide{float(R)});
         } else {
-            // Register-held rows; the row kernel sums the terms per block.
+            // Register-held rows; the row kernel sums the terms per block and
+            // its last block finishes the loss.
 #define VC_XENT_ROWS(NV)                                                                                       \
     launch((xent_rows_cached_kernel<NV>), dim3(cached_grid), dim3(kBlock), 0, d.stream, logits, targets, R, C, \
-           row_stats, part.as<double>())
+           row_stats, part.as<double>(), loss)
             if (nv <= 1) VC_XENT_ROWS(1);
             else if (nv <= 2) VC_XENT_ROWS(2);
             else if (nv <= 4) VC_XENT_ROWS(4);
             else if (nv <= 8) VC_XENT_ROWS(8);
             else VC_XENT_ROWS(16);
 #undef VC_XENT_ROWS
-            blocks = cached_grid;
         }
-        after_launch("xent_forward");
-        launch(red::sum_final_kernel<NegateDivide>, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), loss,
-               blocks, NegateDivide{float(R)});
         after_launch("xent_forward");
         p.done();
     });

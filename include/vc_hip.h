@@ -160,6 +160,55 @@ int vc_hip_div_backward(const float* grad, const float* a, const size_t* a_shape
                         size_t a_rank, const float* b, const size_t* b_shape, const size_t* b_strides,
                         size_t b_rank, const size_t* out_shape, size_t out_rank, float* grad_a, float* grad_b);
 
+/* ---- fused elementwise programs -------------------------------------------- */
+/* One pass of straight-line fp32 code over same-shape contiguous buffers of
+ * rows * cols elements. No counterpart in the reference: the reference runs
+ * each elementwise backward rule (src/ops.cpp:98-154, 363-411), each gradient
+ * accumulation (src/tensor.cpp:281-288) and each bias reduction
+ * (src/autograd.cpp:50-72) as a separate pass; a chain of them becomes one
+ * program here, which reads every input element once and writes only the
+ * values still needed.
+ *
+ * Slots: inputs[j] is loaded into slot j (j < n_inputs), constants[c] is slot
+ * n_inputs + c; the other slots are temporaries. Instruction word:
+ * op | a << 8 | b << 16 | dst << 24, computing slot[dst] = slot[a] op slot[b]
+ * in fp32 (NEG and STEP read only a: -a, and a > 0 ? 1 : 0). A slot is read
+ * only after it is written, constants are never written. outputs[j] receives
+ * slot output_slots[j]; sums[s] ([cols]) receives the column sums of slot
+ * sum_slots[s] viewed as [rows][cols], added in double in a fixed order and
+ * rounded once (the reference's reduce_axis, src/cpu/cpu_backend.cpp:420-441).
+ * Each output value is the same bits as the chain of single-operation kernels
+ * that the program's instructions restate. Output buffers must not overlap
+ * inputs or each other. */
+#define VC_HIP_MAP_SLOTS 16
+#define VC_HIP_MAP_CODE 32
+#define VC_HIP_MAP_INPUTS 8
+#define VC_HIP_MAP_CONSTANTS 8
+#define VC_HIP_MAP_OUTPUTS 4
+#define VC_HIP_MAP_SUMS 2
+#define VC_MAP_ADD 0
+#define VC_MAP_SUB 1
+#define VC_MAP_MUL 2
+#define VC_MAP_DIV 3
+#define VC_MAP_NEG 4
+#define VC_MAP_STEP 5
+typedef struct vc_hip_map_program {
+    const float* inputs[VC_HIP_MAP_INPUTS];
+    size_t n_inputs;
+    float constants[VC_HIP_MAP_CONSTANTS];
+    size_t n_constants;
+    uint32_t code[VC_HIP_MAP_CODE];
+    size_t n_code;
+    float* outputs[VC_HIP_MAP_OUTPUTS];
+    unsigned char output_slots[VC_HIP_MAP_OUTPUTS];
+    size_t n_outputs;
+    float* sums[VC_HIP_MAP_SUMS];
+    unsigned char sum_slots[VC_HIP_MAP_SUMS];
+    size_t n_sums;
+    size_t rows, cols;
+} vc_hip_map_program;
+int vc_hip_map(const vc_hip_map_program* program);
+
 /* ---- matrix multiply ------------------------------------------------------- */
 /* MetalBackend::matmul (metal_backend.hpp:34-40): for z < batch,
  * c[z*m*n ...] = op(a + a_offsets[z]) @ op(b + b_offsets[z]); op transposes

@@ -14,6 +14,7 @@ from ._vectorcore import (  # noqa: F401
     hip_available,
     hip_defer_products,
     hip_device_name,
+    hip_fuse_elementwise,
     hip_gemm_kernel,
     hip_set_gemm_kernel,
     hip_pool_stats,

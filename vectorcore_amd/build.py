@@ -29,7 +29,10 @@ OBJ = PKG / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["runtime.hip", "elementwise.hip", "reduce.hip", "xent.hip", "gemm.hip"]
+HIP_SOURCES = ["runtime.hip", "elementwise.hip", "reduce.hip", "xent.hip", "gemm.hip", "fused_map.hip"]
+# Sources compiled once per define set: the fused-map interpreters, one object
+# per input count, so that they compile in parallel.
+HIP_VARIANT_SOURCES = {"fused_map_inputs.hip": [[f"-DVC_MAP_NIN={k}"] for k in range(1, 9)]}
 LIB_SOURCES = ["shape.cpp", "storage.cpp", "tensor.cpp", "autograd.cpp", "ops.cpp", "nn.cpp",
                "cpu/parallel.cpp", "cpu/cpu_backend.cpp", "hip/hip_backend.cpp"]
 BINDINGS = "python/bindings.cpp"
@@ -63,14 +66,20 @@ def build_hip(verbose: bool = False) -> Path:
     """Compile the HIP kernels and the C ABI into libvc_hip.so."""
     OBJ.mkdir(exist_ok=True)
 
-    def compile_one(src: str) -> Path:
-        obj = OBJ / (Path(src).stem + ".hip.o")
-        log = _run([HIPCC, *HIP_FLAGS, "-c", str(CSRC / "hip" / src), "-o", str(obj)])
+    def compile_one(job) -> Path:
+        src, defines, tag = job
+        obj = OBJ / (Path(src).stem + tag + ".hip.o")
+        log = _run([HIPCC, *HIP_FLAGS, *defines, "-c", str(CSRC / "hip" / src), "-o", str(obj)])
         if verbose and log:
             print(log, file=sys.stderr)
         return obj
 
-    objs = _parallel(compile_one, HIP_SOURCES)
+    jobs = [(src, [], "") for src in HIP_SOURCES]
+    for src, define_sets in HIP_VARIANT_SOURCES.items():
+        jobs += [(src, d, "_" + "_".join(x.split("=")[-1] for x in d)) for d in define_sets]
+    # The slowest compiles (the interpreters) first.
+    jobs.sort(key=lambda j: 0 if j[0] in HIP_VARIANT_SOURCES else 1)
+    objs = _parallel(compile_one, jobs)
     out = PKG / "libvc_hip.so"
     tmp = out.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])

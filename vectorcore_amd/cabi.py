@@ -27,6 +27,48 @@ _szp = ctypes.POINTER(ctypes.c_size_t)
 _i = ctypes.c_int
 _f = ctypes.c_float
 
+# Fused elementwise programs (vc_hip_map).
+MAP_ADD, MAP_SUB, MAP_MUL, MAP_DIV, MAP_NEG, MAP_STEP = range(6)
+MAP_SLOTS, MAP_CODE, MAP_INPUTS, MAP_CONSTANTS, MAP_OUTPUTS, MAP_SUMS = 16, 32, 8, 8, 4, 2
+
+
+class MapProgram(ctypes.Structure):
+    _fields_ = [("inputs", _vp * MAP_INPUTS), ("n_inputs", _sz), ("constants", _f * MAP_CONSTANTS),
+                ("n_constants", _sz), ("code", ctypes.c_uint32 * MAP_CODE), ("n_code", _sz),
+                ("outputs", _vp * MAP_OUTPUTS), ("output_slots", ctypes.c_ubyte * MAP_OUTPUTS), ("n_outputs", _sz),
+                ("sums", _vp * MAP_SUMS), ("sum_slots", ctypes.c_ubyte * MAP_SUMS), ("n_sums", _sz),
+                ("rows", _sz), ("cols", _sz)]
+
+
+def map_word(op: int, a: int, b: int, dst: int) -> int:
+    """One instruction of a vc_hip_map program: slot[dst] = slot[a] op slot[b]."""
+    return op | a << 8 | b << 16 | dst << 24
+
+
+def map_program(inputs, constants, code, outputs, sums, rows, cols) -> MapProgram:
+    """A vc_hip_map program. inputs: device pointers; constants: floats;
+    code: (op, a, b, dst) tuples; outputs and sums: (device pointer, slot) pairs."""
+    p = MapProgram()
+    for j, ptr in enumerate(inputs):
+        p.inputs[j] = ptr
+    p.n_inputs = len(inputs)
+    for j, v in enumerate(constants):
+        p.constants[j] = v
+    p.n_constants = len(constants)
+    for k, ins in enumerate(code):
+        p.code[k] = map_word(*ins)
+    p.n_code = len(code)
+    for j, (ptr, slot) in enumerate(outputs):
+        p.outputs[j] = ptr
+        p.output_slots[j] = slot
+    p.n_outputs = len(outputs)
+    for j, (ptr, slot) in enumerate(sums):
+        p.sums[j] = ptr
+        p.sum_slots[j] = slot
+    p.n_sums = len(sums)
+    p.rows, p.cols = rows, cols
+    return p
+
 _SIGNATURES = {
     "vc_hip_available": ([], _i),
     "vc_hip_device_name": ([], ctypes.c_char_p),
@@ -55,6 +97,7 @@ _SIGNATURES = {
     "vc_hip_exp_backward": ([_vp, _vp, _vp, _sz], _i),
     "vc_hip_log_backward": ([_vp, _vp, _vp, _sz], _i),
     "vc_hip_div_backward": ([_vp, _vp, _szp, _szp, _sz, _vp, _szp, _szp, _sz, _szp, _sz, _vp, _vp], _i),
+    "vc_hip_map": ([ctypes.POINTER(MapProgram)], _i),
     "vc_hip_matmul": ([_vp, _vp, _vp, _sz, _sz, _sz, _szp, _szp, _sz, _i, _i], _i),
     "vc_hip_matmul_relu_mask": ([_vp, _vp, _vp, _sz, _sz, _sz, _szp, _szp, _sz, _i, _i, _vp], _i),
     "vc_hip_matmul_relu_mask_colsum": ([_vp, _vp, _vp, _sz, _sz, _sz, _i, _i, _vp, _vp], _i),

@@ -12,10 +12,13 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cstdint>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 
 namespace vectorcore {
 
@@ -61,6 +64,26 @@ struct DeferredProduct {
     }
 };
 
+// One value of a deferred elementwise expression: an input buffer (a whole
+// or offset view of a computed storage, `count` elements like the
+// expression), a constant, or one fp32 operation (VC_MAP_*) on two values
+// (b == a for the one-operand operations). Nodes are shared between the
+// expressions built on them.
+struct MapNode {
+    enum class Kind { Input, Constant, Op };
+    Kind kind = Kind::Op;
+    int op = 0;
+    std::shared_ptr<MapNode> a, b;
+    std::shared_ptr<HipStorage> input;
+    std::size_t offset = 0;
+    float value = 0.0F;
+};
+using MapExpr = std::shared_ptr<MapNode>;
+
+bool expr_reads(const MapNode& n, const HipStorage* s);
+void expr_replace(MapNode& n, const HipStorage* s, const std::shared_ptr<HipStorage>& with);
+void run_maps(const std::vector<HipStorage*>& outputs);
+
 class HipStorage final : public Storage, public std::enable_shared_from_this<HipStorage> {
 public:
     // A fresh pooled buffer of `elements` floats (contents undefined).
@@ -75,6 +98,12 @@ public:
         : elements_(elements), deferred_(std::make_unique<DeferredProduct>(std::move(product))), shadow_valid_(false) {}
     // Takes over a pooled buffer that already holds this storage's contents.
     HipStorage(std::size_t elements, void* buffer) : elements_(elements), ptr_(buffer), shadow_valid_(false) {}
+    // The values of a deferred elementwise expression (computed on first use
+    // or by HipBackend::flush_elementwise).
+    HipStorage(std::size_t elements, MapExpr expr) : elements_(elements), map_(std::move(expr)), shadow_valid_(false) {}
+    // The column sums of a deferred expression viewed as [rows, elements].
+    HipStorage(std::size_t elements, MapExpr expr, std::size_t rows)
+        : elements_(elements), sum_of_(std::move(expr)), sum_rows_(rows), shadow_valid_(false) {}
 
     ~HipStorage() override {
         if (mirror_) (void)vc_hip_mirror_release(mirror_);
@@ -90,6 +119,10 @@ public:
     // on first use.
     float* ptr() const {
         std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        if (map_ || sum_of_) {
+            run_maps({const_cast<HipStorage*>(this)});
+            return static_cast<float*>(ptr_);
+        }
         if (!ptr_) {
             check(vc_hip_alloc(bytes(), &ptr_), "HIP allocation failed");
             if (!shadow_.empty()) check(vc_hip_upload(ptr_, shadow_.data(), shadow_.size() * sizeof(float)), "HIP upload failed");
@@ -161,7 +194,23 @@ public:
         return *deferred_;
     }
 
-    // Records `reader` as a deferred product that reads this storage.
+    // The pending elementwise expression of this storage, if any.
+    MapExpr map_expr() const {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        return map_;
+    }
+    MapExpr sum_expr() const { return sum_of_; }
+    std::size_t sum_rows() const { return sum_rows_; }
+    bool map_pending() const { return map_ != nullptr || sum_of_ != nullptr; }
+    // Takes the buffer a program wrote this storage's values into, and drops
+    // the expression (and with it the references to its inputs).
+    void set_computed(void* buffer) {
+        ptr_ = buffer;
+        map_.reset();
+        sum_of_.reset();
+    }
+
+    // Records `reader` as a deferred product or expression that reads this storage.
     void add_reader(const std::shared_ptr<HipStorage>& reader) {
         std::lock_guard<std::recursive_mutex> lock(state_mutex());
         readers_.erase(std::remove_if(readers_.begin(), readers_.end(), [](const auto& w) { return w.expired(); }),
@@ -189,7 +238,7 @@ public:
         std::vector<std::shared_ptr<HipStorage>> waiting;
         for (const auto& w : readers_) {
             auto r = w.lock();
-            if (r && r->deferred_ && r->deferred_->reads(this)) waiting.push_back(std::move(r));
+            if (r && r.get() != this && r->reads_pending(this)) waiting.push_back(std::move(r));
         }
         if (waiting.empty()) {
             readers_.clear();
@@ -207,7 +256,9 @@ public:
         auto previous = std::make_shared<HipStorage>(elements_, ptr_);  // takes over the current buffer
         ptr_ = fresh_buffer;
         for (const auto& r : waiting) {
-            r->deferred_->replace(this, previous);
+            if (r->deferred_) r->deferred_->replace(this, previous);
+            if (r->map_) expr_replace(*r->map_, this, previous);
+            if (r->sum_of_) expr_replace(*r->sum_of_, this, previous);
             previous->readers_.push_back(r);
         }
         readers_.clear();
@@ -216,11 +267,18 @@ public:
 
 private:
     std::size_t bytes() const { return (elements_ ? elements_ : 1) * sizeof(float); }
+    // Does work still deferred on this storage read s?
+    bool reads_pending(const HipStorage* s) const {
+        return (deferred_ && deferred_->reads(s)) || (map_ && expr_reads(*map_, s)) || (sum_of_ && expr_reads(*sum_of_, s));
+    }
 
     std::size_t elements_;
     mutable void* ptr_ = nullptr;
     std::vector<float> shadow_;
     mutable std::unique_ptr<DeferredProduct> deferred_;
+    mutable MapExpr map_;     // deferred elementwise values
+    mutable MapExpr sum_of_;  // deferred column sums of this expression
+    std::size_t sum_rows_ = 0;
     std::vector<std::weak_ptr<HipStorage>> readers_;
     vc_hip_mirror* mirror_ = nullptr;  // published value of a one-element result
     mutable std::shared_ptr<HipStorage> column_sum_;  // see set_column_sum
@@ -251,6 +309,305 @@ void require(const HipBackend& b) {
 }
 
 int binary_code(cpu::BinaryOp op) { return static_cast<int>(op); }
+
+// ---- deferred elementwise expressions ------------------------------------------
+// During a backward pass (an ElementwiseScope on this thread), the elementwise
+// rules on same-shape contiguous operands record expressions instead of
+// launching one kernel per operation. An expression is computed by one
+// vc_hip_map program when its storage is first read, or, together with every
+// other expression of the pass that is still referenced, when the pass ends
+// (flush_elementwise); intermediate results that only fed other expressions
+// are never written. A column sum (the bias gradient, sum_to_shape) of an
+// expression becomes one more output of the program.
+
+void collect(const MapNode* n, std::unordered_map<const MapNode*, int>& seen, std::vector<const MapNode*>& order) {
+    if (seen.count(n)) return;
+    seen.emplace(n, 0);
+    if (n->kind == MapNode::Kind::Op) {
+        collect(n->a.get(), seen, order);
+        collect(n->b.get(), seen, order);
+    }
+    order.push_back(n);
+}
+
+bool expr_reads(const MapNode& root, const HipStorage* s) {
+    std::unordered_map<const MapNode*, int> seen;
+    std::vector<const MapNode*> order;
+    collect(&root, seen, order);
+    for (const MapNode* n : order)
+        if (n->kind == MapNode::Kind::Input && n->input.get() == s) return true;
+    return false;
+}
+
+void expr_replace(MapNode& root, const HipStorage* s, const std::shared_ptr<HipStorage>& with) {
+    std::unordered_map<const MapNode*, int> seen;
+    std::vector<const MapNode*> order;
+    collect(&root, seen, order);
+    for (const MapNode* n : order)
+        if (n->kind == MapNode::Kind::Input && n->input.get() == s) const_cast<MapNode*>(n)->input = with;
+}
+
+// A vc_hip_map program for a set of expressions (roots), with slots assigned
+// by liveness: inputs in [0, n_in), constants next, every operation's result
+// in the lowest slot free at that point (an input's slot is free after its
+// last use). Fails when the expressions need more inputs, constants,
+// instructions or slots than one program has.
+struct MapPlan {
+    std::vector<const MapNode*> inputs;  // one node per distinct (storage, offset)
+    std::vector<float> constants;
+    std::vector<std::uint32_t> code;
+    std::unordered_map<const MapNode*, int> root_slot;
+};
+
+bool plan_program(const std::vector<const MapNode*>& roots, MapPlan& plan) {
+    std::unordered_map<const MapNode*, int> seen;
+    std::vector<const MapNode*> order;
+    for (const MapNode* r : roots) collect(r, seen, order);
+    std::vector<const MapNode*> ops;
+    std::vector<std::pair<const HipStorage*, std::size_t>> input_keys;
+    std::vector<std::uint32_t> const_bits;
+    std::unordered_map<const MapNode*, int> vid;  // value id: input index, then constants, then op index
+    for (const MapNode* n : order) {
+        if (n->kind == MapNode::Kind::Input) {
+            const std::pair<const HipStorage*, std::size_t> key{n->input.get(), n->offset};
+            auto it = std::find(input_keys.begin(), input_keys.end(), key);
+            if (it == input_keys.end()) {
+                input_keys.push_back(key);
+                plan.inputs.push_back(n);
+                it = input_keys.end() - 1;
+            }
+            vid[n] = static_cast<int>(it - input_keys.begin());
+        } else if (n->kind == MapNode::Kind::Constant) {
+            std::uint32_t bits = 0;
+            std::memcpy(&bits, &n->value, sizeof bits);
+            auto it = std::find(const_bits.begin(), const_bits.end(), bits);
+            if (it == const_bits.end()) {
+                const_bits.push_back(bits);
+                plan.constants.push_back(n->value);
+                it = const_bits.end() - 1;
+            }
+            vid[n] = -1 - static_cast<int>(it - const_bits.begin());  // resolved below
+        } else {
+            ops.push_back(n);
+        }
+    }
+    const int n_in = static_cast<int>(plan.inputs.size()), n_const = static_cast<int>(plan.constants.size());
+    if (n_in < 1 || n_in > VC_HIP_MAP_INPUTS || n_const > VC_HIP_MAP_CONSTANTS || n_in + n_const > VC_HIP_MAP_SLOTS ||
+        ops.size() > VC_HIP_MAP_CODE)
+        return false;
+    for (auto& [n, v] : vid)
+        if (v < 0) v = n_in + (-1 - v);
+    for (std::size_t k = 0; k < ops.size(); ++k) vid[ops[k]] = n_in + n_const + static_cast<int>(k);
+    // Last instruction reading each value; roots are read at the end.
+    const int values = n_in + n_const + static_cast<int>(ops.size());
+    std::vector<int> last_use(static_cast<std::size_t>(values), -1);
+    for (std::size_t k = 0; k < ops.size(); ++k) {
+        last_use[static_cast<std::size_t>(vid[ops[k]->a.get()])] = static_cast<int>(k);
+        last_use[static_cast<std::size_t>(vid[ops[k]->b.get()])] = static_cast<int>(k);
+    }
+    for (const MapNode* r : roots) last_use[static_cast<std::size_t>(vid[r])] = static_cast<int>(ops.size());
+    std::vector<int> slot(static_cast<std::size_t>(values), -1);
+    std::vector<bool> busy(VC_HIP_MAP_SLOTS, false);
+    for (int v = 0; v < n_in + n_const; ++v) {
+        slot[static_cast<std::size_t>(v)] = v;
+        busy[static_cast<std::size_t>(v)] = true;
+    }
+    for (std::size_t k = 0; k < ops.size(); ++k) {
+        const int va = vid[ops[k]->a.get()], vb = vid[ops[k]->b.get()];
+        const int sa = slot[static_cast<std::size_t>(va)], sb = slot[static_cast<std::size_t>(vb)];
+        for (const int v : {va, vb}) {  // operands read for the last time free their slots (not constants)
+            const bool constant = v >= n_in && v < n_in + n_const;
+            if (!constant && last_use[static_cast<std::size_t>(v)] == static_cast<int>(k))
+                busy[static_cast<std::size_t>(slot[static_cast<std::size_t>(v)])] = false;
+        }
+        int d = -1;
+        for (int t = 0; t < VC_HIP_MAP_SLOTS && d < 0; ++t)
+            if (!busy[static_cast<std::size_t>(t)] && !(t >= n_in && t < n_in + n_const)) d = t;
+        if (d < 0) return false;
+        busy[static_cast<std::size_t>(d)] = true;
+        slot[static_cast<std::size_t>(n_in + n_const + static_cast<int>(k))] = d;
+        plan.code.push_back(static_cast<std::uint32_t>(ops[k]->op) | static_cast<std::uint32_t>(sa) << 8 |
+                            static_cast<std::uint32_t>(sb) << 16 | static_cast<std::uint32_t>(d) << 24);
+    }
+    for (const MapNode* r : roots) plan.root_slot[r] = slot[static_cast<std::size_t>(vid[r])];
+    return true;
+}
+
+bool fits(const std::vector<const MapNode*>& roots) {
+    MapPlan plan;
+    return plan_program(roots, plan);
+}
+
+// Computes pending storages with one program: expressions (map outputs) and
+// column sums, all over the same number of elements (and, for sums, the same
+// columns). The caller holds the state mutex.
+void run_maps(const std::vector<HipStorage*>& requested) {
+    std::vector<HipStorage*> outputs;
+    for (HipStorage* o : requested)
+        if (o->map_pending()) outputs.push_back(o);
+    std::vector<const MapNode*> roots;
+    std::size_t count = 0, rows = 0, cols = 0;
+    std::size_t n_out = 0, n_sum = 0;
+    for (HipStorage* o : outputs) {
+        if (MapExpr m = o->map_expr()) {
+            roots.push_back(m.get());
+            count = o->size();
+            ++n_out;
+        } else if (MapExpr e = o->sum_expr()) {
+            roots.push_back(e.get());
+            rows = o->sum_rows();
+            cols = o->size();
+            count = rows * cols;
+            ++n_sum;
+        }
+    }
+    if (roots.empty()) return;
+    MapPlan plan;
+    if (n_out > VC_HIP_MAP_OUTPUTS || n_sum > VC_HIP_MAP_SUMS || !plan_program(roots, plan))
+        throw std::logic_error("deferred elementwise expression exceeds one program");
+    vc_hip_map_program prog{};
+    for (std::size_t j = 0; j < plan.inputs.size(); ++j)
+        prog.inputs[j] = plan.inputs[j]->input->ptr() + plan.inputs[j]->offset;
+    prog.n_inputs = plan.inputs.size();
+    for (std::size_t c = 0; c < plan.constants.size(); ++c) prog.constants[c] = plan.constants[c];
+    prog.n_constants = plan.constants.size();
+    for (std::size_t k = 0; k < plan.code.size(); ++k) prog.code[k] = plan.code[k];
+    prog.n_code = plan.code.size();
+    std::vector<void*> buffers;
+    auto release_all = [&] {
+        for (void* b : buffers) (void)vc_hip_release(b);
+    };
+    for (std::size_t i = 0; i < outputs.size(); ++i) {
+        void* b = nullptr;
+        const int status = vc_hip_alloc((outputs[i]->size() ? outputs[i]->size() : 1) * sizeof(float), &b);
+        if (status != VC_HIP_OK) {
+            release_all();
+            throw_status(status, "HIP allocation failed");
+        }
+        buffers.push_back(b);
+        const unsigned char slot = static_cast<unsigned char>(plan.root_slot[roots[i]]);
+        if (outputs[i]->map_expr()) {
+            prog.outputs[prog.n_outputs] = static_cast<float*>(b);
+            prog.output_slots[prog.n_outputs++] = slot;
+        } else {
+            prog.sums[prog.n_sums] = static_cast<float*>(b);
+            prog.sum_slots[prog.n_sums++] = slot;
+        }
+    }
+    if (n_sum > 0) {
+        prog.rows = rows;
+        prog.cols = cols;
+    } else {
+        prog.rows = 1;
+        prog.cols = count;
+    }
+    const int status = count || n_sum ? vc_hip_map(&prog) : VC_HIP_OK;
+    if (status != VC_HIP_OK) {
+        release_all();
+        throw_status(status, "HIP fused elementwise pass failed");
+    }
+    for (std::size_t i = 0; i < outputs.size(); ++i) outputs[i]->set_computed(buffers[i]);
+}
+
+// Per-thread state of deferred expressions: inside an ElementwiseScope?
+// And the storages recorded since the scope began, for flush_elementwise.
+thread_local int t_elementwise_depth = 0;
+thread_local std::vector<std::weak_ptr<HipStorage>> t_pending;
+
+std::atomic<bool>& fuse_flag() {
+    static std::atomic<bool> flag{[] {
+        const char* v = std::getenv("VECTORCORE_HIP_FUSE");
+        return !(v && std::string(v) == "0");
+    }()};
+    return flag;
+}
+
+bool deferring() { return t_elementwise_depth > 0 && fuse_flag().load(); }
+
+// The expression of an operand: its own when it is a whole pending
+// expression of `count` values, otherwise an input node over its buffer
+// (computed now if it is still deferred).
+MapExpr operand_expr(const Storage& s, std::size_t offset, std::size_t count) {
+    const auto& h = as_hip(s);
+    if (offset == 0 && count == h.size())
+        if (MapExpr m = h.map_expr()) return m;
+    auto n = std::make_shared<MapNode>();
+    n->kind = MapNode::Kind::Input;
+    (void)h.ptr();
+    n->input = std::const_pointer_cast<HipStorage>(h.shared_from_this());
+    n->offset = offset;
+    return n;
+}
+
+MapExpr constant_expr(float value) {
+    auto n = std::make_shared<MapNode>();
+    n->kind = MapNode::Kind::Constant;
+    n->value = value;
+    return n;
+}
+
+MapExpr op_expr(int op, MapExpr a, MapExpr b) {
+    auto n = std::make_shared<MapNode>();
+    n->op = op;
+    n->a = std::move(a);
+    n->b = b ? std::move(b) : n->a;
+    return n;
+}
+
+// Every storage an expression reads as an input.
+void expr_inputs(const MapNode& root, std::vector<std::shared_ptr<HipStorage>>& out) {
+    std::unordered_map<const MapNode*, int> seen;
+    std::vector<const MapNode*> order;
+    collect(&root, seen, order);
+    for (const MapNode* n : order)
+        if (n->kind == MapNode::Kind::Input &&
+            std::find(out.begin(), out.end(), n->input) == out.end())
+            out.push_back(n->input);
+}
+
+std::shared_ptr<HipStorage> pending_storage(std::size_t elements, MapExpr expr, std::size_t sum_rows = 0) {
+    auto out = sum_rows ? std::make_shared<HipStorage>(elements, expr, sum_rows)
+                        : std::make_shared<HipStorage>(elements, expr);
+    std::vector<std::shared_ptr<HipStorage>> inputs;
+    expr_inputs(*expr, inputs);
+    for (const auto& in : inputs) in->add_reader(out);
+    t_pending.push_back(out);
+    return out;
+}
+
+// A deferred elementwise operation on `count` values: build(x...) makes the
+// expression from the operands' expressions. When the combined expression
+// does not fit one program, the operands are computed first (from the
+// largest) and become inputs.
+template <typename Build>
+std::shared_ptr<Storage> deferred_map(std::size_t count, std::vector<std::pair<const Storage*, std::size_t>> operands,
+                                      Build build) {
+    std::lock_guard<std::recursive_mutex> lock(state_mutex());
+    for (std::size_t round = 0; round <= operands.size(); ++round) {
+        std::vector<MapExpr> ex;
+        for (const auto& [s, off] : operands) ex.push_back(operand_expr(*s, off, count));
+        MapExpr e = build(ex);
+        if (fits({e.get()})) return pending_storage(count, std::move(e));
+        // Compute the operand expression with the most operations first.
+        std::size_t worst = operands.size(), worst_ops = 0;
+        for (std::size_t i = 0; i < operands.size(); ++i) {
+            const MapExpr& x = ex[i];
+            if (x->kind != MapNode::Kind::Op) continue;
+            std::unordered_map<const MapNode*, int> seen;
+            std::vector<const MapNode*> order;
+            collect(x.get(), seen, order);
+            if (order.size() > worst_ops) {
+                worst_ops = order.size();
+                worst = i;
+            }
+        }
+        if (worst == operands.size()) break;
+        (void)as_hip(*operands[worst].first).ptr();
+    }
+    throw std::logic_error("elementwise expression does not fit one program");
+}
+
+bool contiguous(const Shape& shape, const Strides& strides) { return strides == contiguous_strides(shape); }
 
 }  // namespace
 
@@ -318,6 +675,12 @@ std::shared_ptr<Storage> HipBackend::binary(const Storage& a, std::size_t a_offs
     if (b_shape == out_shape && numel(a_shape) == 1) {
         if (auto s = hip_host_scalar(a)) return binary_scalar(b, b_offset, count, *s, true, operation);
     }
+    if (deferring() && count > 0 && a_shape == out_shape && b_shape == out_shape && contiguous(a_shape, a_strides) &&
+        contiguous(b_shape, b_strides)) {
+        const int op = binary_code(operation);  // VC_MAP_ADD..VC_MAP_DIV share the binary codes
+        return deferred_map(count, {{&a, a_offset}, {&b, b_offset}},
+                            [op](std::vector<MapExpr>& x) { return op_expr(op, x[0], x[1]); });
+    }
     auto out = fresh(count);
     if (count == 0) return out;
     check(vc_hip_binary(dptr(a, a_offset), a_shape.data(), a_strides.data(), a_shape.size(), dptr(b, b_offset),
@@ -330,6 +693,12 @@ std::shared_ptr<Storage> HipBackend::binary(const Storage& a, std::size_t a_offs
 std::shared_ptr<Storage> HipBackend::binary_scalar(const Storage& a, std::size_t a_offset, std::size_t count, float s,
                                                    bool scalar_first, cpu::BinaryOp operation) {
     require(*this);
+    if (deferring() && count > 0) {
+        const int op = binary_code(operation);
+        return deferred_map(count, {{&a, a_offset}}, [op, s, scalar_first](std::vector<MapExpr>& x) {
+            return scalar_first ? op_expr(op, constant_expr(s), x[0]) : op_expr(op, x[0], constant_expr(s));
+        });
+    }
     auto out = fresh(count);
     if (count == 0) return out;
     check(vc_hip_binary_scalar(dptr(a, a_offset), count, s, scalar_first ? 1 : 0, out->ptr(), binary_code(operation)),
@@ -340,6 +709,12 @@ std::shared_ptr<Storage> HipBackend::binary_scalar(const Storage& a, std::size_t
 std::shared_ptr<Storage> HipBackend::unary(const Storage& input, std::size_t offset, std::size_t count,
                                            cpu::UnaryOp operation) {
     require(*this);
+    if (deferring() && count > 0 &&
+        (operation == cpu::UnaryOp::Negate || operation == cpu::UnaryOp::ReluGradient)) {
+        const int op = operation == cpu::UnaryOp::Negate ? VC_MAP_NEG : VC_MAP_STEP;
+        return deferred_map(count, {{&input, offset}},
+                            [op](std::vector<MapExpr>& x) { return op_expr(op, x[0], nullptr); });
+    }
     auto out = fresh(count);
     if (count == 0) return out;
     check(vc_hip_unary(dptr(input, offset), out->ptr(), count, static_cast<int>(operation)), "HIP unary op failed");
@@ -439,6 +814,11 @@ std::shared_ptr<Storage> HipBackend::reduce_axis(const Storage& input, std::size
     if (operation == cpu::ReduceOp::Sum && outer == 1 && offset == 0) {
         // Column sums the kernel that wrote the input already produced.
         if (auto sums = as_hip(input).take_column_sum(length, inner)) return sums;
+        // Column sums of a pending expression: one more output of its program.
+        if (deferring() && length > 0 && inner >= 64 && length * inner == input.size()) {
+            std::lock_guard<std::recursive_mutex> lock(state_mutex());
+            if (MapExpr e = as_hip(input).map_expr()) return pending_storage(inner, e, length);
+        }
     }
     auto out = fresh(outer * inner);
     if (outer * inner == 0) return out;
@@ -507,6 +887,55 @@ std::atomic<bool>& defer_flag() {
 
 void HipBackend::set_defer_products(bool enable) { defer_flag() = enable; }
 bool HipBackend::defer_products() const { return defer_flag(); }
+
+void HipBackend::set_fuse_elementwise(bool enable) { fuse_flag() = enable; }
+bool HipBackend::fuse_elementwise() const { return fuse_flag(); }
+
+HipBackend::ElementwiseScope::ElementwiseScope() {
+    if (t_elementwise_depth++ == 0) t_pending.clear();
+}
+HipBackend::ElementwiseScope::~ElementwiseScope() {
+    if (--t_elementwise_depth == 0) t_pending.clear();  // what is still pending is computed on first use
+}
+
+void HipBackend::flush_elementwise() {
+    std::lock_guard<std::recursive_mutex> lock(state_mutex());
+    std::vector<std::shared_ptr<HipStorage>> live;
+    for (const auto& w : t_pending)
+        if (auto p = w.lock(); p && p->map_pending()) live.push_back(std::move(p));
+    t_pending.clear();
+    // Groups over the same elements: a column sum with the expressions it
+    // can share a pass with, then the remaining expressions, as many per
+    // program as fit.
+    std::vector<bool> done(live.size(), false);
+    auto elements_of = [](const HipStorage& h) { return h.sum_expr() ? h.sum_rows() * h.size() : h.size(); };
+    for (int sums_first = 1; sums_first >= 0; --sums_first) {
+        for (std::size_t i = 0; i < live.size(); ++i) {
+            if (done[i] || (sums_first != 0) != (live[i]->sum_expr() != nullptr)) continue;
+            std::vector<HipStorage*> group{live[i].get()};
+            std::vector<const MapNode*> roots{live[i]->sum_expr() ? live[i]->sum_expr().get() : live[i]->map_expr().get()};
+            std::size_t n_out = live[i]->sum_expr() ? 0 : 1, n_sum = live[i]->sum_expr() ? 1 : 0;
+            done[i] = true;
+            for (std::size_t j = i + 1; j < live.size(); ++j) {
+                if (done[j] || elements_of(*live[j]) != elements_of(*live[i])) continue;
+                const bool sum = live[j]->sum_expr() != nullptr;
+                if (sum && (n_sum == VC_HIP_MAP_SUMS || (n_sum > 0 && live[j]->size() != group[0]->size()) ||
+                            (n_sum == 0)))
+                    continue;
+                if (!sum && n_out == VC_HIP_MAP_OUTPUTS) continue;
+                roots.push_back(sum ? live[j]->sum_expr().get() : live[j]->map_expr().get());
+                if (!fits(roots)) {
+                    roots.pop_back();
+                    continue;
+                }
+                group.push_back(live[j].get());
+                (sum ? n_sum : n_out) += 1;
+                done[j] = true;
+            }
+            run_maps(group);
+        }
+    }
+}
 
 std::shared_ptr<Storage> HipBackend::matmul_deferred(const std::shared_ptr<Storage>& a, std::size_t a_offset,
                                                      const std::shared_ptr<Storage>& b, std::size_t b_offset,
@@ -590,6 +1019,20 @@ std::shared_ptr<Storage> HipBackend::activation_backward(Activation kind, const 
                                                          const Storage& saved, std::size_t saved_offset,
                                                          std::size_t count) {
     require(*this);
+    if (deferring() && count > 0) {
+        // The same fp32 operations as the fused kernels below.
+        return deferred_map(count, {{&grad, grad_offset}, {&saved, saved_offset}}, [kind](std::vector<MapExpr>& x) {
+            switch (kind) {
+                case Activation::Relu: return op_expr(VC_MAP_MUL, x[0], op_expr(VC_MAP_STEP, x[1], nullptr));
+                case Activation::Sigmoid:
+                    return op_expr(VC_MAP_MUL, op_expr(VC_MAP_MUL, x[0], x[1]),
+                                   op_expr(VC_MAP_SUB, constant_expr(1.0F), x[1]));
+                case Activation::Exp: return op_expr(VC_MAP_MUL, x[0], x[1]);
+                case Activation::Log: return op_expr(VC_MAP_DIV, x[0], x[1]);
+            }
+            throw std::logic_error("unknown activation");
+        });
+    }
     auto out = fresh(count);
     if (count == 0) return out;
     const float* g = dptr(grad, grad_offset);
@@ -611,6 +1054,21 @@ std::pair<std::shared_ptr<Storage>, std::shared_ptr<Storage>> HipBackend::divide
     const Shape& out_shape, bool need_a, bool need_b) {
     require(*this);
     const std::size_t count = numel(out_shape);
+    if (deferring() && count > 0 && a_shape == out_shape && b_shape == out_shape && contiguous(a_shape, a_strides) &&
+        contiguous(b_shape, b_strides)) {
+        // grad / b and -(grad * a) / (b * b), as div_backward_kernel computes them.
+        std::shared_ptr<Storage> da, db;
+        if (need_a)
+            da = deferred_map(count, {{&grad, grad_offset}, {&b, b_offset}},
+                              [](std::vector<MapExpr>& x) { return op_expr(VC_MAP_DIV, x[0], x[1]); });
+        if (need_b)
+            db = deferred_map(count, {{&grad, grad_offset}, {&a, a_offset}, {&b, b_offset}},
+                              [](std::vector<MapExpr>& x) {
+                                  return op_expr(VC_MAP_DIV, op_expr(VC_MAP_NEG, op_expr(VC_MAP_MUL, x[0], x[1]), nullptr),
+                                                 op_expr(VC_MAP_MUL, x[2], x[2]));
+                              });
+        return {da, db};
+    }
     std::shared_ptr<HipStorage> ga = need_a ? fresh(count) : nullptr;
     std::shared_ptr<HipStorage> gb = need_b ? fresh(count) : nullptr;
     if (count && (need_a || need_b)) {

@@ -108,6 +108,29 @@ public:
     void set_defer_products(bool enable);
     [[nodiscard]] bool defer_products() const;
 
+    // --- deferred elementwise expressions ---
+    // While an ElementwiseScope is alive on this thread (the autograd engine
+    // opens one for a backward pass), binary, binary_scalar, negate and
+    // ReLU-gradient unary ops, activation_backward and divide_backward on
+    // same-shape contiguous operands, and column sums of their results
+    // (reduce_axis, outer 1), record an expression instead of launching a
+    // kernel. A storage holding one is computed by one vc_hip_map program on
+    // first use; flush_elementwise computes every such storage of the scope
+    // still referenced, those over the same elements in one program, and the
+    // intermediate values nothing references any more are never written.
+    // Values are the same bits as the eager kernels'. On by default;
+    // VECTORCORE_HIP_FUSE=0 or set_fuse_elementwise(false) keeps every op eager.
+    class ElementwiseScope {
+    public:
+        ElementwiseScope();
+        ~ElementwiseScope();
+        ElementwiseScope(const ElementwiseScope&) = delete;
+        ElementwiseScope& operator=(const ElementwiseScope&) = delete;
+    };
+    void flush_elementwise();
+    void set_fuse_elementwise(bool enable);
+    [[nodiscard]] bool fuse_elementwise() const;
+
     // --- fused kernels used by the hip arm of the backward rules ---
     [[nodiscard]] std::shared_ptr<Storage> fill(std::size_t count, float value);
     // out = a op s (scalar_first false) or s op a; s is a host value.

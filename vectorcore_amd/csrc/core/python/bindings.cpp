@@ -251,6 +251,17 @@ PYBIND11_MODULE(_vectorcore, m) {
         py::arg("enable") = py::none(),
         "Whether 2-D hip products are computed on first use (fusing a following bias add and ReLU); "
         "sets it when `enable` is given and returns the previous setting.");
+    m.def(
+        "hip_fuse_elementwise",
+        [](std::optional<bool> enable) {
+            auto& b = HipBackend::instance();
+            const bool previous = b.fuse_elementwise();
+            if (enable) b.set_fuse_elementwise(*enable);
+            return previous;
+        },
+        py::arg("enable") = py::none(),
+        "Whether a hip backward pass evaluates its chains of elementwise gradient ops (and their bias column "
+        "sums) as fused programs; sets it when `enable` is given and returns the previous setting.");
     m.def("hip_profile_reset", [] { check(vc_hip_profile_reset()); });
     m.def("hip_profile_read", [] {
         std::size_t n = 0;

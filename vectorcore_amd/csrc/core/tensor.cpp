@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <iomanip>
+#include <optional>
 #include <random>
 #include <sstream>
 #include <stdexcept>
@@ -254,6 +255,11 @@ void Tensor::backward() const {
     backward(Tensor::ones(shape(), false, device()));
 }
 
+namespace {
+void run_backward(const std::shared_ptr<detail::TensorImpl>& root,
+                  const std::vector<std::shared_ptr<detail::TensorImpl>>& order, const Tensor& gradient);
+}  // namespace
+
 // Reverse-mode engine (the semantics of src/tensor.cpp:251-301): nodes in
 // depth-first post-order over grad_fn parents, walked in reverse; each node's
 // summed upstream gradient is consumed and dropped once used; leaves and
@@ -282,16 +288,31 @@ void Tensor::backward(const Tensor& gradient) const {
         stack.pop_back();
     }
 
+    NoGradGuard guard;
+    // On hip, the elementwise rules of this pass record expressions; the ones
+    // still referenced when the pass ends (leaf and retained gradients) are
+    // computed together by flush_elementwise below.
+    std::optional<HipBackend::ElementwiseScope> fusion;
+    if (gradient.device() == Device::hip()) fusion.emplace();
+    run_backward(impl_, order, gradient);
+    if (fusion) HipBackend::instance().flush_elementwise();
+}
+
+namespace {
+
+// The node loop of Tensor::backward over `order` (depth-first post-order from
+// root), seeded with `gradient` at root.
+void run_backward(const std::shared_ptr<detail::TensorImpl>& root,
+                  const std::vector<std::shared_ptr<detail::TensorImpl>>& order, const Tensor& gradient) {
     // How many graph nodes feed a gradient to each node.
     std::unordered_map<detail::TensorImpl*, int> consumers;
     for (const auto& node : order)
         if (node->grad_fn)
             for (const auto& parent : node->grad_fn->parents) ++consumers[parent.get()];
 
-    NoGradGuard guard;
     std::unordered_map<detail::TensorImpl*, Tensor> pending;
     std::unordered_set<detail::TensorImpl*> premasked;  // ReLU outputs whose gradient arrived masked
-    pending.emplace(impl_.get(), gradient.detach());
+    pending.emplace(root.get(), gradient.detach());
     for (auto it = order.rbegin(); it != order.rend(); ++it) {
         const auto& node = *it;
         auto found = pending.find(node.get());
@@ -344,6 +365,8 @@ void Tensor::backward(const Tensor& gradient) const {
         }
     }
 }
+
+}  // namespace
 
 std::string Tensor::repr() const {
     std::ostringstream s;

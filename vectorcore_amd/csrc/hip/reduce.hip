@@ -165,13 +165,14 @@ __global__ __launch_bounds__(kBlock) void cols_kernel(const float* __restrict__ 
 // a0 + r, a0 + r + 16, ... of the segment, sixteen rows in flight. A wave
 // holds four row lanes of the same columns (lanes c, c + 16, c + 32, c + 48):
 // they are joined with two exchanges (lane ^ 16, then lane ^ 32), then the
-// four waves in wave order through LDS. One partial per (segment, column).
+// four waves in wave order through LDS. One partial per (segment, column);
+// with a single segment (Direct), the sum itself, rounded to float, in out.
 constexpr int kColLanes = 16, kRowLanes = 16, kColInFlight = 16;
 
-template <bool Vec>
+template <bool Vec, bool Direct>
 __global__ __launch_bounds__(kBlock) void colsum_tile_kernel(const float* __restrict__ x, double* __restrict__ part,
-                                                             int64_t outer, int64_t len, int64_t inner, int64_t seg_len,
-                                                             int64_t chunks) {
+                                                             float* __restrict__ out, int64_t outer, int64_t len,
+                                                             int64_t inner, int64_t seg_len, int64_t chunks) {
     constexpr int W = Vec ? 4 : 1;
     constexpr int kWaves = kBlock / kWave;
     __shared__ double lds[kWaves][kColLanes * W];
@@ -229,7 +230,10 @@ __global__ __launch_bounds__(kBlock) void colsum_tile_kernel(const float* __rest
             double total = lds[0][c * W + w];
 #pragma unroll
             for (int k = 1; k < kWaves; ++k) total += lds[k][c * W + w];
-            if (col + w < inner) part[(s * outer + o) * inner + col + w] = total;
+            if (col + w < inner) {
+                if constexpr (Direct) out[o * inner + col + w] = float(total);
+                else part[(s * outer + o) * inner + col + w] = total;
+            }
         }
     }
 }
@@ -329,7 +333,8 @@ void check_i32(int64_t v, const char* what) {
 
 // Segments of a column sum: a function of the shape only; aim at ~512
 // long-running workgroups (two per CU), at least 128 rows per segment, at
-// most 64 segments.
+// most 64 segments. A reduction of at most 2^17 elements takes one segment
+// and one launch: its time is the launches', not the bytes'.
 struct ColumnPlan {
     bool vec;
     int64_t chunks, segs, seg_len;
@@ -344,6 +349,7 @@ ColumnPlan column_plan(const float* in, int64_t outer, int64_t len, int64_t inne
     if (blocks_x > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, "reduction too large");
     int64_t segs = std::max<int64_t>(1, (512 + blocks_x - 1) / blocks_x);
     segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / 128), int64_t(kMaxColSegs)});
+    if (outer * len * inner <= (int64_t(1) << 17)) segs = 1;
     c.seg_len = (len + segs - 1) / segs;
     c.segs = (len + c.seg_len - 1) / c.seg_len;
     return c;
@@ -353,12 +359,22 @@ void column_sum(Device& d, const ColumnPlan& c, const float* in, float* out, dou
                 int64_t len, int64_t inner, const char* label) {
     const int64_t total = outer * inner;
     const dim3 grid(static_cast<unsigned>(outer * c.chunks), static_cast<unsigned>(c.segs));
+    if (c.segs == 1) {
+        if (c.vec)
+            launch(colsum_tile_kernel<true, true>, grid, dim3(kBlock), 0, d.stream, in, part, out, outer, len, inner,
+                   c.seg_len, c.chunks);
+        else
+            launch(colsum_tile_kernel<false, true>, grid, dim3(kBlock), 0, d.stream, in, part, out, outer, len, inner,
+                   c.seg_len, c.chunks);
+        after_launch(label);
+        return;
+    }
     if (c.vec)
-        launch(colsum_tile_kernel<true>, grid, dim3(kBlock), 0, d.stream, in, part, outer, len, inner, c.seg_len,
-               c.chunks);
+        launch(colsum_tile_kernel<true, false>, grid, dim3(kBlock), 0, d.stream, in, part, out, outer, len, inner,
+               c.seg_len, c.chunks);
     else
-        launch(colsum_tile_kernel<false>, grid, dim3(kBlock), 0, d.stream, in, part, outer, len, inner, c.seg_len,
-               c.chunks);
+        launch(colsum_tile_kernel<false, false>, grid, dim3(kBlock), 0, d.stream, in, part, out, outer, len, inner,
+               c.seg_len, c.chunks);
     after_launch(label);
     launch(colsum_combine_kernel, dim3(unsigned((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, d.stream, part, out,
            total, int(c.segs));

@@ -115,11 +115,11 @@ __device__ inline float wave_min(float v) {
 }
 
 // Row statistics and loss term of one row from values in registers (NV
-// float4 per lane; element a = 4 lane + 256 u + component, a multiple-of-4
-// row of at most 256 NV classes; elements past the row hold -inf). Each lane
-// visits its elements in ascending order, as the streaming path does, so both
-// give the same bits. Returns the loss term on lane 0.
-template <int NV>
+// float4 per lane; element a = 4 lane + 256 u + component, a row of at most
+// 256 NV classes; elements past the row hold -inf). Each lane visits its
+// elements in ascending order, as the streaming path does, so both give the
+// same bits. Returns the loss term on lane 0.
+template <bool Vec, int NV>
 __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, int t, int lane,
                                    float* __restrict__ stats) {
     // The reference's max is the first strict maximum, skipping NaN after
@@ -132,9 +132,18 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
         mx = __builtin_fmaxf(__builtin_fmaxf(mx, v[u].x), __builtin_fmaxf(__builtin_fmaxf(v[u].y, v[u].z), v[u].w));
-        const bool in_row = lane * 4 + u * kWave * 4 < len;  // a whole float4 of the row, or of padding
-        const float lo = __builtin_fminf(__builtin_fminf(v[u].x, v[u].y), __builtin_fminf(v[u].z, v[u].w));
-        mn = in_row ? __builtin_fminf(mn, lo) : mn;
+        // The minimum leaves the padding past the row out: whole float4s of it
+        // (Vec: the row is a multiple of 4), or single elements.
+        const int a = lane * 4 + u * kWave * 4, n = int(len);
+        if constexpr (Vec) {
+            const float lo = __builtin_fminf(__builtin_fminf(v[u].x, v[u].y), __builtin_fminf(v[u].z, v[u].w));
+            mn = a < n ? __builtin_fminf(mn, lo) : mn;
+        } else {
+            const float inf = __builtin_inff();
+            const float lo = __builtin_fminf(__builtin_fminf(a < n ? v[u].x : inf, a + 1 < n ? v[u].y : inf),
+                                             __builtin_fminf(a + 2 < n ? v[u].z : inf, a + 3 < n ? v[u].w : inf));
+            mn = __builtin_fminf(mn, lo);
+        }
     }
     mx = wave_max(mx);
     const float first = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v[0].x)));
@@ -182,8 +191,14 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
             const int a = lane * 4 + u * kWave * 4;
             if (a < len) {
                 const float s0 = v[u].x - m, s1 = v[u].y - m, s2 = v[u].z - m, s3 = v[u].w - m;
-                bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) | (a + 2 != t && !isfinite(s2)) |
-                       (a + 3 != t && !isfinite(s3));
+                if constexpr (Vec) {  // whole float4s of the row
+                    bad |= (a != t && !isfinite(s0)) | (a + 1 != t && !isfinite(s1)) | (a + 2 != t && !isfinite(s2)) |
+                           (a + 3 != t && !isfinite(s3));
+                } else {
+                    const int n = int(len);
+                    bad |= (a != t && !isfinite(s0)) | (a + 1 < n && a + 1 != t && !isfinite(s1)) |
+                           (a + 2 < n && a + 2 != t && !isfinite(s2)) | (a + 3 < n && a + 3 != t && !isfinite(s3));
+                }
             }
         }
     }
@@ -203,13 +218,21 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
     return lane == 0 ? write_row(r, len, t, x_t, m, acc, bad, stats) : 0.0f;
 }
 
-template <int NV>
+// Loads a row into registers, -inf past its end. Vec: 16-byte loads (len a
+// multiple of 4, row 16-byte aligned); otherwise four scalar loads per float4,
+// the same values in the same places.
+template <bool Vec, int NV>
 __device__ inline void load_row(f4 (&v)[NV], const float* __restrict__ row, int64_t len, int lane) {
+    const float pad = -__builtin_inff();
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
         const int64_t a = int64_t(lane) * 4 + int64_t(u) * kWave * 4;
-        const float pad = -__builtin_inff();
-        v[u] = a < len ? ld4(row + a) : f4{pad, pad, pad, pad};
+        if constexpr (Vec) {
+            v[u] = a < len ? ld4(row + a) : f4{pad, pad, pad, pad};
+        } else {
+            v[u] = f4{a < len ? row[a] : pad, a + 1 < len ? row[a + 1] : pad, a + 2 < len ? row[a + 2] : pad,
+                      a + 3 < len ? row[a + 3] : pad};
+        }
     }
 }
 
@@ -244,7 +267,7 @@ struct NegateDivide {
     }
 };
 
-template <int NV>
+template <int NV, bool Vec>
 // Six waves per SIMD (at most 80 registers) fit without spilling and measured
 // 2-10% faster than the unconstrained allocation (4 waves); eight spill.
 __global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float* __restrict__ x,
@@ -259,16 +282,16 @@ __global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float
     double total = 0.0;  // lane 0: this wavefront's terms, in row order
     if (first < rows) {
         f4 cur[NV], next[NV];
-        load_row(cur, x + first * len, len, lane);
+        load_row<Vec>(cur, x + first * len, len, lane);
         int t = __builtin_amdgcn_readfirstlane(targets[first]);
         for (int64_t r = first; r < rows; r += waves) {
             const int64_t rn = r + waves;
             int tn = 0;
             if (rn < rows) {
-                load_row(next, x + rn * len, len, lane);
+                load_row<Vec>(next, x + rn * len, len, lane);
                 tn = __builtin_amdgcn_readfirstlane(targets[rn]);
             }
-            total += double(finish_row(cur, r, len, t, lane, stats));
+            total += double(finish_row<Vec>(cur, r, len, t, lane, stats));
 #pragma unroll
             for (int u = 0; u < NV; ++u) cur[u] = next[u];
             t = tn;
@@ -404,7 +427,7 @@ __global__ __launch_bounds__(kBlock) void xent_backward_kernel(const float* __re
 // same bits as xent_backward_kernel's.
 constexpr int kColRows = 16;
 
-template <int NV>
+template <int NV, bool Vec>
 __global__ __launch_bounds__(kBlock) void xent_backward_colsum_kernel(const float* __restrict__ x,
                                                                       const int* __restrict__ targets,
                                                                       const float* __restrict__ stats,
@@ -422,9 +445,9 @@ __global__ __launch_bounds__(kBlock) void xent_backward_colsum_kernel(const floa
     const int64_t last = std::min<int64_t>(rows, int64_t(blockIdx.x + 1) * kColRows);
     if (first < last) {
         f4 cur[NV], next[NV];
-        load_row(cur, x + first * len, len, lane);
+        load_row<Vec>(cur, x + first * len, len, lane);
         for (int64_t r = first; r < last; r += kRowsPerBlock) {
-            if (r + kRowsPerBlock < last) load_row(next, x + (r + kRowsPerBlock) * len, len, lane);
+            if (r + kRowsPerBlock < last) load_row<Vec>(next, x + (r + kRowsPerBlock) * len, len, lane);
             const float m = stats[2 * r], s = stats[2 * r + 1];
             const float scale = c / s;
             const int t = targets[r];
@@ -438,11 +461,19 @@ __global__ __launch_bounds__(kBlock) void xent_backward_colsum_kernel(const floa
                     g.y = scale * row_exp(cur[u].y - m) + (a + 1 == t ? neg_c : -0.0f);
                     g.z = scale * row_exp(cur[u].z - m) + (a + 2 == t ? neg_c : -0.0f);
                     g.w = scale * row_exp(cur[u].w - m) + (a + 3 == t ? neg_c : -0.0f);
-                    *reinterpret_cast<f4*>(out + a) = g;
+                    if constexpr (Vec) {
+                        *reinterpret_cast<f4*>(out + a) = g;
+                    } else {
+                        out[a] = g.x;
+                        if (a + 1 < len) out[a + 1] = g.y;
+                        if (a + 2 < len) out[a + 2] = g.z;
+                        if (a + 3 < len) out[a + 3] = g.w;
+                    }
+                    // past the row: exp(-inf - m) * scale + -0.0 = +0.0 (or NaN with a NaN m, never stored)
                     acc[u][0] += double(g.x);
-                    acc[u][1] += double(g.y);
-                    acc[u][2] += double(g.z);
-                    acc[u][3] += double(g.w);
+                    acc[u][1] += double(a + 1 < len ? g.y : 0.0f);
+                    acc[u][2] += double(a + 2 < len ? g.z : 0.0f);
+                    acc[u][3] += double(a + 3 < len ? g.w : 0.0f);
                 }
             }
 #pragma unroll
@@ -511,14 +542,14 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         // Rows of up to 4096 classes are held in registers (NV float4 per lane),
         // with at most 8 workgroups per CU walking the rows (6 fit at once at
         // this kernel's register use; 3 to 12 per CU measured within 3%).
-        const int64_t nv = vec ? (C + kWave * 4 - 1) / (kWave * 4) : 0;
+        const int64_t nv = (C + kWave * 4 - 1) / (kWave * 4);
         const unsigned cached_grid = unsigned(std::min<int64_t>(
             {(R + kRowsPerBlock - 1) / kRowsPerBlock, int64_t(d.cu_count) * kXentBlocksPerCu,
              int64_t(kDoneGroup) * kDoneGroups}));
         int64_t blocks = 0;  // loss partials of the streaming path, one double each
         Scratch part(size_t(std::max<int64_t>(cached_grid, (R + red::sum_chunk(R) - 1) / red::sum_chunk(R))) *
                      sizeof(double));
-        if (!vec || nv > 16) {
+        if (nv > 16) {
             // Row terms, then the shared deterministic two-stage sum.
             launch((vec ? xent_rows_kernel<true> : xent_rows_kernel<false>), dim3(grid), dim3(kBlock), 0, d.stream,
                    logits, targets, R, C, row_stats, terms.as<float>());
@@ -533,9 +564,9 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         } else {
             // Register-held rows; the row kernel sums the terms per block and
             // its last block finishes the loss.
-#define VC_XENT_ROWS(NV)                                                                                       \
-    launch((xent_rows_cached_kernel<NV>), dim3(cached_grid), dim3(kBlock), 0, d.stream, logits, targets, R, C, \
-           row_stats, part.as<double>(), loss)
+#define VC_XENT_ROWS(NV)                                                                                          \
+    launch(vec ? xent_rows_cached_kernel<NV, true> : xent_rows_cached_kernel<NV, false>, dim3(cached_grid),     \
+           dim3(kBlock), 0, d.stream, logits, targets, R, C, row_stats, part.as<double>(), loss)
             if (nv <= 1) VC_XENT_ROWS(1);
             else if (nv <= 2) VC_XENT_ROWS(2);
             else if (nv <= 4) VC_XENT_ROWS(4);
@@ -571,7 +602,8 @@ int vc_hip_xent_backward_colsum(const float* logits, const int32_t* targets, con
         if (classes > size_t(std::numeric_limits<int>::max())) fail(VC_HIP_ERR_OVERFLOW, "too many classes");
         const int64_t R = int64_t(rows), C = int64_t(classes);
         const int64_t nv = (C + kWave * 4 - 1) / (kWave * 4);
-        const bool fused = rows > 0 && C % 4 == 0 && nv <= 8 && aligned16(logits) && aligned16(grad_logits);
+        const bool fused = rows > 0 && nv <= 8;
+        const bool vec = C % 4 == 0 && aligned16(logits) && aligned16(grad_logits);
         if (!fused) {  // the plain backward, then a separate reduction of dx
             xent_backward(logits, targets, row_stats, grad_loss, grad_loss_value, rows, classes, grad_logits);
             const int rc = vc_hip_reduce_axis(grad_logits, column_sum, 1, rows, classes, VC_REDUCE_SUM);
@@ -583,9 +615,10 @@ int vc_hip_xent_backward_colsum(const float* logits, const int32_t* targets, con
         Scratch part(size_t(blocks) * size_t(C) * sizeof(double));
         {
             Profiled p("xent_backward", 0.0, 8.0 * double(R * C) + 12.0 * double(R) + 8.0 * double(blocks * C));
-#define VC_XENT_BWD_COLSUM(NV)                                                                                    \
-    launch((xent_backward_colsum_kernel<NV>), dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, logits, targets, \
-           row_stats, grad_loss, grad_loss_value, R, C, grad_logits, part.as<double>())
+#define VC_XENT_BWD_COLSUM(NV)                                                                               \
+    launch(vec ? xent_backward_colsum_kernel<NV, true> : xent_backward_colsum_kernel<NV, false>,               \
+           dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, logits, targets, row_stats, grad_loss,           \
+           grad_loss_value, R, C, grad_logits, part.as<double>())
             if (nv <= 1) VC_XENT_BWD_COLSUM(1);
             else if (nv <= 2) VC_XENT_BWD_COLSUM(2);
             else if (nv <= 4) VC_XENT_BWD_COLSUM(4);

@@ -103,16 +103,18 @@ __device__ inline float wave_max(float v) {
     return o > v ? o : v;
 }
 
-// Smallest value over the wavefront (inputs never NaN).
-__device__ inline float wave_min(float v) {
+// Largest unsigned value over the wavefront.
+__device__ inline uint32_t wave_umax(uint32_t v) {
     const int lane = red::lane_id();
-    v = __builtin_fminf(v, red::partner<0>(v, lane));
-    v = __builtin_fminf(v, red::partner<1>(v, lane));
-    v = __builtin_fminf(v, red::partner<2>(v, lane));
-    v = __builtin_fminf(v, red::partner<3>(v, lane));
-    v = __builtin_fminf(v, red::partner<4>(v, lane));
-    return __builtin_fminf(v, red::partner<5>(v, lane));
+    v = max(v, red::partner<0>(v, lane));
+    v = max(v, red::partner<1>(v, lane));
+    v = max(v, red::partner<2>(v, lane));
+    v = max(v, red::partner<3>(v, lane));
+    v = max(v, red::partner<4>(v, lane));
+    return max(v, red::partner<5>(v, lane));
 }
+
+__device__ inline uint32_t bits_of(float v) { return __builtin_bit_cast(uint32_t, v); }
 
 // Row statistics and loss term of one row from values in registers (NV
 // float4 per lane; element a = 4 lane + 256 u + component, a row of at most
@@ -125,24 +127,27 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
     // The reference's max is the first strict maximum, skipping NaN after
     // element 0. Its value is the largest non-NaN element, whichever index
     // holds it (fmaxf ignores NaN too), except for the sign of a zero maximum
-    // (the first zero wins) and a NaN element 0, both settled below. The row
-    // minimum (padding left out) tells whether any element is -inf, whose
-    // shifted value is the one non-finite case the exp-sum does not show.
-    float mx = -__builtin_inff(), mn = __builtin_inff();
+    // (the first zero wins) and a NaN element 0, both settled below. The
+    // largest bit pattern of the row (padding left out) tells whether any
+    // element is -inf, whose shifted value is the one non-finite case the
+    // exp-sum does not show: as unsigned integers, -inf (0xff800000) and the
+    // negative NaNs are above every other float. (An integer maximum needs no
+    // NaN handling, which a float minimum costs an instruction per element.)
+    float mx = -__builtin_inff();
+    uint32_t hi = 0;
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
         mx = __builtin_fmaxf(__builtin_fmaxf(mx, v[u].x), __builtin_fmaxf(__builtin_fmaxf(v[u].y, v[u].z), v[u].w));
-        // The minimum leaves the padding past the row out: whole float4s of it
-        // (Vec: the row is a multiple of 4), or single elements.
+        // Padding past the row is left out: whole float4s of it (Vec: the row
+        // is a multiple of 4), or single elements.
         const int a = lane * 4 + u * kWave * 4, n = int(len);
         if constexpr (Vec) {
-            const float lo = __builtin_fminf(__builtin_fminf(v[u].x, v[u].y), __builtin_fminf(v[u].z, v[u].w));
-            mn = a < n ? __builtin_fminf(mn, lo) : mn;
+            const uint32_t b = max(max(bits_of(v[u].x), bits_of(v[u].y)), max(bits_of(v[u].z), bits_of(v[u].w)));
+            hi = a < n ? max(hi, b) : hi;
         } else {
-            const float inf = __builtin_inff();
-            const float lo = __builtin_fminf(__builtin_fminf(a < n ? v[u].x : inf, a + 1 < n ? v[u].y : inf),
-                                             __builtin_fminf(a + 2 < n ? v[u].z : inf, a + 3 < n ? v[u].w : inf));
-            mn = __builtin_fminf(mn, lo);
+            const uint32_t b = max(max(a < n ? bits_of(v[u].x) : 0u, a + 1 < n ? bits_of(v[u].y) : 0u),
+                                   max(a + 2 < n ? bits_of(v[u].z) : 0u, a + 3 < n ? bits_of(v[u].w) : 0u));
+            hi = max(hi, b);
         }
     }
     mx = wave_max(mx);
@@ -169,21 +174,34 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
     // Elements past the row give exp(-inf - m) = 0 (or NaN when m is -inf or
     // NaN, and then every real element's term is NaN too): adding them leaves
     // the sum unchanged.
-    // Four double chains per lane, one per float4 component, joined in
-    // component order: the streaming path adds in the same order.
+    // Four chains per lane, one per float4 component: each adds up to four
+    // terms (float4s u = 4q .. 4q + 3) in fp32, then that partial in double;
+    // the chains are joined in component order, the lanes in double. A
+    // partial of at most four positive terms is within 3 * 2^-24 of its exact
+    // sum, so the row's sum keeps that relative accuracy before its final
+    // rounding to float (a double add per term measured slower: the forward
+    // is bound by instruction issue).
     double c0 = 0.0, c1 = 0.0, c2 = 0.0, c3 = 0.0;
 #pragma unroll
-    for (int u = 0; u < NV; ++u) {
-        c0 += double(row_exp(v[u].x - m));
-        c1 += double(row_exp(v[u].y - m));
-        c2 += double(row_exp(v[u].z - m));
-        c3 += double(row_exp(v[u].w - m));
+    for (int q = 0; q < NV; q += 4) {
+        float f0 = 0.0f, f1 = 0.0f, f2 = 0.0f, f3 = 0.0f;
+#pragma unroll
+        for (int u = q; u < q + 4 && u < NV; ++u) {
+            f0 += row_exp(v[u].x - m);
+            f1 += row_exp(v[u].y - m);
+            f2 += row_exp(v[u].z - m);
+            f3 += row_exp(v[u].w - m);
+        }
+        c0 += double(f0);
+        c1 += double(f1);
+        c2 += double(f2);
+        c3 += double(f3);
     }
     const double acc = red::wave_sum(((c0 + c1) + c2) + c3);
     // Some shifted value is not finite exactly when m is not finite, an
     // element is -inf, or the sum is NaN (a NaN or +inf element makes its own
     // term, or every term, NaN).
-    const bool nonfinite = !isfinite(m) || !(wave_min(mn) > -__builtin_inff()) || acc != acc;
+    const bool nonfinite = !isfinite(m) || wave_umax(hi) >= 0xff800000u || acc != acc;
     int bad = 0;  // a non-target log-prob that is not finite
     if (nonfinite) {  // rare: decide exactly, leaving the target out
 #pragma unroll
@@ -224,10 +242,14 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
 template <bool Vec, int NV>
 __device__ inline void load_row(f4 (&v)[NV], const float* __restrict__ row, int64_t len, int lane) {
     const float pad = -__builtin_inff();
+    const int64_t full = len / (kWave * 4);  // float4 slots inside the row on every lane (wave-uniform)
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
         const int64_t a = int64_t(lane) * 4 + int64_t(u) * kWave * 4;
-        if constexpr (Vec) {
+        if (u < full) {  // no padding to set: a uniform branch instead of per-lane selects
+            if constexpr (Vec) v[u] = ld4(row + a);
+            else v[u] = f4{row[a], row[a + 1], row[a + 2], row[a + 3]};
+        } else if constexpr (Vec) {
             v[u] = a < len ? ld4(row + a) : f4{pad, pad, pad, pad};
         } else {
             v[u] = f4{a < len ? row[a] : pad, a + 1 < len ? row[a + 1] : pad, a + 2 < len ? row[a + 2] : pad,
@@ -281,6 +303,11 @@ __global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float
     const int64_t waves = int64_t(gridDim.x) * kRowsPerBlock;
     double total = 0.0;  // lane 0: this wavefront's terms, in row order
     if (first < rows) {
+        // The next row's target is loaded first and read after this row is
+        // finished, so waiting for it never waits for the row loads. (Two
+        // register sets taking turns instead of the copy below measured 5%
+        // slower: the duplicated row code needs more registers than 6 waves
+        // per SIMD leave.)
         f4 cur[NV], next[NV];
         load_row<Vec>(cur, x + first * len, len, lane);
         int t = __builtin_amdgcn_readfirstlane(targets[first]);
@@ -288,13 +315,13 @@ __global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float
             const int64_t rn = r + waves;
             int tn = 0;
             if (rn < rows) {
+                tn = targets[rn];
                 load_row<Vec>(next, x + rn * len, len, lane);
-                tn = __builtin_amdgcn_readfirstlane(targets[rn]);
             }
             total += double(finish_row<Vec>(cur, r, len, t, lane, stats));
 #pragma unroll
             for (int u = 0; u < NV; ++u) cur[u] = next[u];
-            t = tn;
+            t = __builtin_amdgcn_readfirstlane(tn);
         }
     }
     if (lane == 0) wave_terms[threadIdx.x / kWave] = total;
@@ -445,12 +472,22 @@ __global__ __launch_bounds__(kBlock) void xent_backward_colsum_kernel(const floa
     const int64_t last = std::min<int64_t>(rows, int64_t(blockIdx.x + 1) * kColRows);
     if (first < last) {
         f4 cur[NV], next[NV];
+        // The next row's statistics and target are loaded before its values
+        // and read after this row is stored, so waiting for them never waits
+        // for the row loads in flight.
+        float m = stats[2 * first], s = stats[2 * first + 1];
+        int t = targets[first];
         load_row<Vec>(cur, x + first * len, len, lane);
         for (int64_t r = first; r < last; r += kRowsPerBlock) {
-            if (r + kRowsPerBlock < last) load_row<Vec>(next, x + (r + kRowsPerBlock) * len, len, lane);
-            const float m = stats[2 * r], s = stats[2 * r + 1];
+            float mn = 0.0f, sn = 1.0f;
+            int tn = 0;
+            if (r + kRowsPerBlock < last) {
+                mn = stats[2 * (r + kRowsPerBlock)];
+                sn = stats[2 * (r + kRowsPerBlock) + 1];
+                tn = targets[r + kRowsPerBlock];
+                load_row<Vec>(next, x + (r + kRowsPerBlock) * len, len, lane);
+            }
             const float scale = c / s;
-            const int t = targets[r];
             float* out = dx + r * len;
 #pragma unroll
             for (int u = 0; u < NV; ++u) {
@@ -478,6 +515,9 @@ __global__ __launch_bounds__(kBlock) void xent_backward_colsum_kernel(const floa
             }
 #pragma unroll
             for (int u = 0; u < NV; ++u) cur[u] = next[u];
+            m = mn;
+            s = sn;
+            t = tn;
         }
     }
     if (w > 0) {

@@ -356,8 +356,12 @@ def reduce_axis_dev(x, axis, op):
 
 
 @pytest.mark.parametrize("shape", [(64, 500, 33), (5, 300, 7), (4096, 4096), (8192, 1000), (3, 4, 5), (1, 3_000_001),
-                                   (8, 1024 * 1024)])
+                                   (8, 1024 * 1024), (3001, 2051), (70, 8192), (2049, 2048)])
 def test_reduce_axis_against_oracle(shape):
+    # Column sums of one matrix with at least 2048 columns take the one-launch
+    # kernel (the last block of each column chunk adds the partials):
+    # (4096, 4096) and (2049, 2048) with 16-byte loads, (3001, 2051) with
+    # scalar loads and short last segments, (70, 8192) with 4 segments.
     rng = np.random.default_rng(len(shape) + shape[-1])
     x = rng.standard_normal(shape).astype(np.float32)
     for axis in range(len(shape)):

@@ -238,6 +238,134 @@ __global__ __launch_bounds__(kBlock) void colsum_tile_kernel(const float* __rest
     }
 }
 
+// A column sum (one matrix, outer 1) in one launch. Block (chunk, segment)
+// sums its 16 W columns over the segment's rows as colsum_tile_kernel does
+// (every row of a row lane's share loaded before the first add), writes the
+// partials with device-scope stores, waits for them, and counts itself in on
+// its chunk's counter; the chunk's last block adds the chunk's partials in
+// segment order (256 / (16 W) threads per column, each a contiguous range of
+// segments, their sums then added in range order), writes the float sums and
+// resets the counter for the next launch (launches on the library's stream
+// never overlap). The result does not depend on which block is last.
+constexpr int kMaxFinishChunks = 1 << 16;
+__device__ unsigned int g_colsum_done[kMaxFinishChunks];
+
+template <bool Vec>
+__global__ __launch_bounds__(kBlock) void colsum_finish_kernel(const float* __restrict__ x, double* __restrict__ part,
+                                                               float* __restrict__ out, int64_t len, int64_t inner,
+                                                               int64_t seg_len) {
+    constexpr int W = Vec ? 4 : 1;
+    constexpr int kWaves = kBlock / kWave;
+    constexpr int kCols = kColLanes * W;      // columns of a block
+    constexpr int kParts = kBlock / kCols;    // threads per column in the final sum
+    __shared__ double lds[kWaves][kCols];
+    __shared__ int last_block;
+    const int c = threadIdx.x % kColLanes, rl = threadIdx.x / kColLanes;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int64_t chunk = blockIdx.x, s = blockIdx.y, segs = gridDim.y;
+    const int64_t col = (chunk * kColLanes + c) * W;
+    const int64_t a0 = s * seg_len, a1 = std::min(len, a0 + seg_len);
+    double acc[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) acc[w] = 0.0;
+    if (col < inner) {
+        const float* base = x + col;
+        for (int64_t a = a0 + rl; a < a1; a += kColInFlight * kRowLanes) {
+            // Up to kColInFlight rows, all loaded before the first add.
+            if constexpr (Vec) {
+                f4 v[kColInFlight];
+#pragma unroll
+                for (int u = 0; u < kColInFlight; ++u) {
+                    const int64_t r = a + u * kRowLanes;
+                    v[u] = r < a1 ? ld4(base + r * inner) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+#pragma unroll
+                for (int u = 0; u < kColInFlight; ++u) {
+                    if (a + u * kRowLanes < a1) {
+                        acc[0] += double(v[u].x); acc[1] += double(v[u].y); acc[2] += double(v[u].z); acc[3] += double(v[u].w);
+                    }
+                }
+            } else {
+                float v[kColInFlight];
+#pragma unroll
+                for (int u = 0; u < kColInFlight; ++u) {
+                    const int64_t r = a + u * kRowLanes;
+                    v[u] = r < a1 ? base[r * inner] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < kColInFlight; ++u)
+                    if (a + u * kRowLanes < a1) acc[0] += double(v[u]);
+            }
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        acc[w] += __shfl_xor(acc[w], 16, kWave);
+        acc[w] += __shfl_xor(acc[w], 32, kWave);
+    }
+    if (lane < kColLanes) {
+#pragma unroll
+        for (int w = 0; w < W; ++w) lds[wave][c * W + w] = acc[w];
+    }
+    __syncthreads();
+    if (wave == 0 && lane < kColLanes) {
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            double total = lds[0][c * W + w];
+#pragma unroll
+            for (int k = 1; k < kWaves; ++k) total += lds[k][c * W + w];
+            if (col + w < inner)
+                __hip_atomic_store(&part[s * inner + col + w], total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // A device-scope store is acknowledged once it is visible at device
+        // scope: waiting for every outstanding memory operation orders these
+        // stores before the count below.
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned* counter = &g_colsum_done[chunk];
+        const bool last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
+                          unsigned(segs);
+        if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_block = last;
+    }
+    __syncthreads();
+    if (!last_block) return;
+    // Thread t: column t % kCols of the chunk, segments of range t / kCols.
+    const int cc = int(threadIdx.x) % kCols, q = int(threadIdx.x) / kCols;
+    const int64_t ocol = chunk * kCols + cc;
+    const int64_t per = (segs + kParts - 1) / kParts;
+    const int64_t s0 = std::min<int64_t>(segs, q * per), s1 = std::min<int64_t>(segs, s0 + per);
+    // Device-scope loads (cache policy sc1 = 16), eight in flight; a load
+    // past the partials falls outside the descriptor and reads 0 (not added).
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        part, short(0), int(std::min<int64_t>(segs * inner * int64_t(sizeof(double)), 0x7fffffff)), 0x00020000);
+    double sum = 0.0;
+    if (ocol < inner) {
+        for (int64_t t0 = s0; t0 < s1; t0 += 8) {
+            double v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t t = t0 + u;
+                const int64_t off = t < s1 ? (t * inner + ocol) * int64_t(sizeof(double)) : int64_t(0x7fffffff);
+                v[u] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rp, int(off), 0, 16));
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (t0 + u < s1) sum += v[u];
+        }
+    }
+    __shared__ double range_sum[kParts][kCols];
+    range_sum[q][cc] = sum;
+    __syncthreads();
+    if (q == 0 && ocol < inner) {
+        double total = range_sum[0][cc];
+        for (int k = 1; k < kParts; ++k) total += range_sum[k][cc];
+        out[ocol] = float(total);
+    }
+}
+
 // out[t] = float(sum over segments of part[s][t]), in segment order. All
 // segments' loads are issued before the first add (one memory round trip).
 constexpr int kMaxColSegs = 64;
@@ -355,6 +483,31 @@ ColumnPlan column_plan(const float* in, int64_t outer, int64_t len, int64_t inne
     return c;
 }
 
+// The one-launch column sum (outer 1): about 2048 blocks, segments of at
+// least 16 rows, at most 32 segments (the blocks of a chunk count in on one
+// counter, and atomics on one address are served one at a time: 128 segments
+// per chunk measured 2.5x slower than 32); a function of the shape only.
+// Used from 32 chunks (2048 columns) up: with fewer chunks the blocks are too
+// few to stream the matrix at full rate and the two-launch path is faster
+// (8192 x 1000: 13.6 us against 12.4 us; 8192 x 4096: 23.9 us against 26.1 us).
+constexpr int64_t kFinishMinChunks = 32;
+struct FinishPlan {
+    bool vec;
+    int64_t chunks, segs, seg_len;
+};
+
+FinishPlan finish_plan(const float* in, int64_t len, int64_t inner) {
+    FinishPlan f{};
+    f.vec = inner % 4 == 0 && aligned16(in);
+    const int64_t width = f.vec ? 4 * kColLanes : kColLanes;
+    f.chunks = (inner + width - 1) / width;
+    int64_t segs = std::max<int64_t>(1, (2048 + f.chunks - 1) / f.chunks);
+    segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / 16), int64_t(32)});
+    f.seg_len = (len + segs - 1) / segs;
+    f.segs = (len + f.seg_len - 1) / f.seg_len;
+    return f;
+}
+
 void column_sum(Device& d, const ColumnPlan& c, const float* in, float* out, double* part, int64_t outer,
                 int64_t len, int64_t inner, const char* label) {
     const int64_t total = outer * inner;
@@ -462,6 +615,21 @@ void reduce_axis(const float* in, float* out, int64_t outer, int64_t len, int64_
         after_launch(label);
         p.done();
         return;
+    }
+    if (op == VC_REDUCE_SUM && outer == 1 && len * inner > (int64_t(1) << 17)) {
+        const FinishPlan f = finish_plan(in, len, inner);
+        const int64_t part_bytes = f.segs * inner * int64_t(sizeof(double));
+        if (f.chunks >= kFinishMinChunks && f.chunks <= kMaxFinishChunks && part_bytes < (int64_t(1) << 31)) {
+            double* part = static_cast<double*>(memory.take(size_t(part_bytes)));
+            const dim3 grid(unsigned(f.chunks), unsigned(f.segs));
+            if (f.vec)
+                launch(colsum_finish_kernel<true>, grid, dim3(kBlock), 0, d.stream, in, part, out, len, inner, f.seg_len);
+            else
+                launch(colsum_finish_kernel<false>, grid, dim3(kBlock), 0, d.stream, in, part, out, len, inner, f.seg_len);
+            after_launch(label);
+            p.done();
+            return;
+        }
     }
     if (op == VC_REDUCE_SUM) {
         const ColumnPlan c = column_plan(in, outer, len, inner);

@@ -483,13 +483,15 @@ def test_cross_entropy_forward_back_to_back_calls():
         np.testing.assert_allclose(loss, want, rtol=1e-6, err_msg=f"call {i}: {rows}x{classes}")
 
 
-def test_cross_entropy_vector_and_scalar_loads_agree():
-    # Aligned rows of 1000 classes are loaded into registers with 16-byte
-    # loads, the same rows one float off 16-byte alignment with scalar loads
-    # into the same places; the backward runs its vector and its scalar
-    # kernel. Every path takes its exponentials from one function and adds
-    # them in one order, so statistics, loss and gradients agree bit for bit.
-    xe = W.xent(rows=2000, classes=1000, seed=17)
+@pytest.mark.parametrize("classes", [1000, 2000])
+def test_cross_entropy_vector_and_scalar_loads_agree(classes):
+    # Aligned rows of 1000 classes (two per wavefront) or 2000 (one per
+    # wavefront) are loaded into registers with 16-byte loads, the same rows
+    # one float off 16-byte alignment with scalar loads into the same places;
+    # the backward runs its vector and its scalar kernel. Every path takes its
+    # exponentials from one function and adds them in one order, so
+    # statistics, loss and gradients agree bit for bit.
+    xe = W.xent(rows=2001, classes=classes, seed=17)
     logits, targets = xe["logits"], xe["targets"].astype(np.int32)
     rows, classes = logits.shape
     padded = np.concatenate([np.zeros(1, np.float32), logits.reshape(-1)])
@@ -562,11 +564,12 @@ def _special_rows(classes, rng):
     return np.stack(rows), targets
 
 
-@pytest.mark.parametrize("classes", [1000, 40, 37, 4100])
+@pytest.mark.parametrize("classes", [1000, 40, 37, 2000, 4100])
 def test_cross_entropy_special_values_match_the_oracle(classes):
-    # 1000 and 40 take the register-held row kernel, 37 (not a multiple of 4)
-    # the same kernel with scalar loads and a partial last float4, 4100 (too
-    # long for registers) the streaming one. Each row alone, so
+    # 1000 and 40 take the register-held kernel with two rows per wavefront,
+    # 37 (not a multiple of 4) the same kernel with scalar loads and a partial
+    # last float4, 2000 the kernel with one row per wavefront, 4100 (too long
+    # for registers) the streaming one. Each row alone, so
     # one NaN row does not hide the others; the row maximum must carry the
     # reference's sign of zero.
     from oracle import autograd as A

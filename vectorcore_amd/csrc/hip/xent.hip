@@ -279,6 +279,163 @@ constexpr unsigned kDoneGroup = 64, kDoneGroups = 64, kDoneStride = 32;
 __device__ unsigned int g_xent_group_done[kDoneGroups * kDoneStride];
 __device__ unsigned int g_xent_groups_done;
 
+// ---- two rows per wavefront: lanes 0-31 hold one row, lanes 32-63 the next --
+// For rows of at most 1024 classes. A row's cross-lane reductions then take
+// five exchange steps instead of six, and one instruction serves both rows:
+// the per-row work that does not scale with the row length halves. The row's
+// values are dead after the exp-sum (the target's logit and the rare exact
+// non-finite check read memory again), which keeps the kernel at five waves
+// per SIMD without spilling.
+__device__ inline float half_max(float v) {
+    const int lane = red::lane_id();
+    float o = red::partner<0>(v, lane);
+    v = o > v ? o : v;
+    o = red::partner<1>(v, lane);
+    v = o > v ? o : v;
+    o = red::partner<2>(v, lane);
+    v = o > v ? o : v;
+    o = red::partner<3>(v, lane);
+    v = o > v ? o : v;
+    o = red::partner<4>(v, lane);
+    return o > v ? o : v;
+}
+
+// Sum over the half-wave in a fixed order; every lane of the half gets the same bits.
+__device__ inline double half_sum(double v) {
+    const int lane = red::lane_id();
+    v += red::partner<0>(v, lane);
+    v += red::partner<1>(v, lane);
+    v += red::partner<2>(v, lane);
+    v += red::partner<3>(v, lane);
+    v += red::partner<4>(v, lane);
+    return v;
+}
+
+__device__ inline uint32_t half_umax(uint32_t v) {
+    const int lane = red::lane_id();
+    v = max(v, red::partner<0>(v, lane));
+    v = max(v, red::partner<1>(v, lane));
+    v = max(v, red::partner<2>(v, lane));
+    v = max(v, red::partner<3>(v, lane));
+    return max(v, red::partner<4>(v, lane));
+}
+
+__device__ inline int half_or(int v) {
+    const int lane = red::lane_id();
+    v |= red::partner<0>(v, lane);
+    v |= red::partner<1>(v, lane);
+    v |= red::partner<2>(v, lane);
+    v |= red::partner<3>(v, lane);
+    v |= red::partner<4>(v, lane);
+    return v;
+}
+
+__device__ inline Best half_best(Best b) {
+    const int lane = red::lane_id();
+    b = red::combine_partner<0>(b, lane);
+    b = red::combine_partner<1>(b, lane);
+    b = red::combine_partner<2>(b, lane);
+    b = red::combine_partner<3>(b, lane);
+    return red::combine_partner<4>(b, lane);
+}
+
+// A row of at most 128 NV classes into the registers of one half-wave: lane
+// hl of the half holds element a = 4 hl + 128 u + component (-inf past the row).
+template <bool Vec, int NV>
+__device__ inline void load_half_row(f4 (&v)[NV], const float* __restrict__ row, int64_t len, int hl) {
+    const float pad = -__builtin_inff();
+    const int64_t full = len / 128;  // slots inside the row on every lane (wave-uniform)
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int64_t a = int64_t(hl) * 4 + int64_t(u) * 128;
+        if (u < full) {
+            if constexpr (Vec) v[u] = ld4(row + a);
+            else v[u] = f4{row[a], row[a + 1], row[a + 2], row[a + 3]};
+        } else if constexpr (Vec) {
+            v[u] = a < len ? ld4(row + a) : f4{pad, pad, pad, pad};
+        } else {
+            v[u] = f4{a < len ? row[a] : pad, a + 1 < len ? row[a + 1] : pad, a + 2 < len ? row[a + 2] : pad,
+                      a + 3 < len ? row[a + 3] : pad};
+        }
+    }
+}
+
+// finish_row for the row (at `row` in memory, index r) held by this lane's
+// half-wave; t is its target, the same on the half's 32 lanes. valid false:
+// a padding row past the batch, whose results are not written. Returns the
+// loss term on the half's lane 0, as the same arithmetic as finish_row does
+// with a half-wave's lanes.
+template <bool Vec, int NV>
+__device__ inline float finish_half_row(const f4 (&v)[NV], int64_t r, bool valid, const float* __restrict__ row,
+                                        int64_t len, int t, int lane, float* __restrict__ stats) {
+    const int hl = lane & 31;
+    const bool t_in_row = t >= 0 && int64_t(t) < len;
+    const float x_t = t_in_row ? row[t] : 0.0f;  // loaded now, used at the end
+    float mx = -__builtin_inff();
+    uint32_t hi = 0;
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        mx = __builtin_fmaxf(__builtin_fmaxf(mx, v[u].x), __builtin_fmaxf(__builtin_fmaxf(v[u].y, v[u].z), v[u].w));
+        const int a = hl * 4 + u * 128, n = int(len);
+        if constexpr (Vec) {
+            const uint32_t b = max(max(bits_of(v[u].x), bits_of(v[u].y)), max(bits_of(v[u].z), bits_of(v[u].w)));
+            hi = a < n ? max(hi, b) : hi;
+        } else {
+            const uint32_t b = max(max(a < n ? bits_of(v[u].x) : 0u, a + 1 < n ? bits_of(v[u].y) : 0u),
+                                   max(a + 2 < n ? bits_of(v[u].z) : 0u, a + 3 < n ? bits_of(v[u].w) : 0u));
+            hi = max(hi, b);
+        }
+    }
+    mx = half_max(mx);
+    // Element 0 of each half's row is on that half's lane 0.
+    const float f0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[0].x), 0));
+    const float f1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[0].x), 32));
+    const float first = lane >= 32 ? f1 : f0;
+    float m;
+    if (first != first) {
+        m = first;  // max() keeps a NaN first element (src/cpu/cpu_backend.cpp:443-452)
+    } else if (mx == 0.0f) {  // rare: which zero comes first
+        Best b = red::no_best();
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const int a = hl * 4 + u * 128;
+            if (a < len) {
+                red::consider_ordered(b, v[u].x, a);
+                red::consider_ordered(b, v[u].y, a + 1);
+                red::consider_ordered(b, v[u].z, a + 2);
+                red::consider_ordered(b, v[u].w, a + 3);
+            }
+        }
+        m = half_best(b).v;
+    } else {
+        m = mx;
+    }
+    double c0 = 0.0, c1 = 0.0, c2 = 0.0, c3 = 0.0;  // as in finish_row
+#pragma unroll
+    for (int q = 0; q < NV; q += 4) {
+        float g0 = 0.0f, g1 = 0.0f, g2 = 0.0f, g3 = 0.0f;
+#pragma unroll
+        for (int u = q; u < q + 4 && u < NV; ++u) {
+            g0 += row_exp(v[u].x - m);
+            g1 += row_exp(v[u].y - m);
+            g2 += row_exp(v[u].z - m);
+            g3 += row_exp(v[u].w - m);
+        }
+        c0 += double(g0);
+        c1 += double(g1);
+        c2 += double(g2);
+        c3 += double(g3);
+    }
+    const double acc = half_sum(((c0 + c1) + c2) + c3);
+    const bool nonfinite = !isfinite(m) || half_umax(hi) >= 0xff800000u || acc != acc;
+    int bad = 0;  // a non-target log-prob that is not finite
+    if (nonfinite) {  // rare: decide exactly from memory, leaving the target out
+        for (int64_t a = hl; a < len; a += 32) bad |= (a != t && !isfinite(row[a] - m));
+    }
+    bad = half_or(bad);
+    return (hl == 0 && valid) ? write_row(r, len, t, x_t, m, acc, bad, stats) : 0.0f;
+}
+
 // loss = -(float)(sum of row terms) / (float)rows: negate, then divide, as
 // -(...).sum() / batch evaluates (src/nn.cpp:52).
 struct NegateDivide {
@@ -289,42 +446,15 @@ struct NegateDivide {
     }
 };
 
-template <int NV, bool Vec>
-// Six waves per SIMD (at most 80 registers) fit without spilling and measured
-// 2-10% faster than the unconstrained allocation (4 waves); eight spill.
-__global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float* __restrict__ x,
-                                                                  const int* __restrict__ targets, int64_t rows,
-                                                                  int64_t len, float* __restrict__ stats,
-                                                                  double* __restrict__ part, float* __restrict__ loss) {
-    __shared__ double wave_terms[kRowsPerBlock];
+// The end of a one-launch forward: each wavefront's loss terms are in
+// wave_terms. Block b adds them in wave order into part[b] with a
+// device-scope store, waits for it, and counts itself in on its group's
+// counter; the block completing a group counts the group in on the top
+// counter, and the block completing the last group adds all partials in
+// block order, writes the loss and resets the counters.
+__device__ inline void finish_loss(double* wave_terms, double* __restrict__ part, int64_t rows,
+                                   float* __restrict__ loss) {
     __shared__ int last_block;
-    const int lane = threadIdx.x % kWave;
-    const int64_t first = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
-    const int64_t waves = int64_t(gridDim.x) * kRowsPerBlock;
-    double total = 0.0;  // lane 0: this wavefront's terms, in row order
-    if (first < rows) {
-        // The next row's target is loaded first and read after this row is
-        // finished, so waiting for it never waits for the row loads. (Two
-        // register sets taking turns instead of the copy below measured 5%
-        // slower: the duplicated row code needs more registers than 6 waves
-        // per SIMD leave.)
-        f4 cur[NV], next[NV];
-        load_row<Vec>(cur, x + first * len, len, lane);
-        int t = __builtin_amdgcn_readfirstlane(targets[first]);
-        for (int64_t r = first; r < rows; r += waves) {
-            const int64_t rn = r + waves;
-            int tn = 0;
-            if (rn < rows) {
-                tn = targets[rn];
-                load_row<Vec>(next, x + rn * len, len, lane);
-            }
-            total += double(finish_row<Vec>(cur, r, len, t, lane, stats));
-#pragma unroll
-            for (int u = 0; u < NV; ++u) cur[u] = next[u];
-            t = __builtin_amdgcn_readfirstlane(tn);
-        }
-    }
-    if (lane == 0) wave_terms[threadIdx.x / kWave] = total;
     __syncthreads();
     if (threadIdx.x == 0) {
         double sum = wave_terms[0];
@@ -370,6 +500,77 @@ __global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float
         loss[0] = NegateDivide{float(rows)}(float(sum));
         __hip_atomic_store(&g_xent_groups_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+template <int NV, bool Vec>
+// Six waves per SIMD (at most 80 registers) fit without spilling and measured
+// 2-10% faster than the unconstrained allocation (4 waves); eight spill.
+__global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float* __restrict__ x,
+                                                                  const int* __restrict__ targets, int64_t rows,
+                                                                  int64_t len, float* __restrict__ stats,
+                                                                  double* __restrict__ part, float* __restrict__ loss) {
+    __shared__ double wave_terms[kRowsPerBlock];
+    const int lane = threadIdx.x % kWave;
+    const int64_t first = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
+    const int64_t waves = int64_t(gridDim.x) * kRowsPerBlock;
+    double total = 0.0;  // lane 0: this wavefront's terms, in row order
+    if (first < rows) {
+        // The next row's target is loaded first and read after this row is
+        // finished, so waiting for it never waits for the row loads. (Two
+        // register sets taking turns instead of the copy below measured 5%
+        // slower: the duplicated row code needs more registers than 6 waves
+        // per SIMD leave.)
+        f4 cur[NV], next[NV];
+        load_row<Vec>(cur, x + first * len, len, lane);
+        int t = __builtin_amdgcn_readfirstlane(targets[first]);
+        for (int64_t r = first; r < rows; r += waves) {
+            const int64_t rn = r + waves;
+            int tn = 0;
+            if (rn < rows) {
+                tn = targets[rn];
+                load_row<Vec>(next, x + rn * len, len, lane);
+            }
+            total += double(finish_row<Vec>(cur, r, len, t, lane, stats));
+#pragma unroll
+            for (int u = 0; u < NV; ++u) cur[u] = next[u];
+            t = __builtin_amdgcn_readfirstlane(tn);
+        }
+    }
+    if (lane == 0) wave_terms[threadIdx.x / kWave] = total;
+    finish_loss(wave_terms, part, rows, loss);
+}
+
+// Rows of at most 1024 classes, two per wavefront (finish_half_row): wave w
+// takes row pairs p = w, w + W, ... (rows 2p and 2p + 1). The loss terms are
+// summed per half in row order, then the wavefront's lower half before its
+// upper half, then as xent_rows_cached_kernel does (its last block finishes
+// the loss). Five waves per SIMD (96 registers) fit without spilling and
+// measured faster than six (which spill) or loading the next pair ahead (three
+// waves): 32768 x 1000 in 22.8 us against 25.8 us for a row per wavefront.
+template <int NV, bool Vec>
+__global__ __launch_bounds__(kBlock, 5) void xent_half_rows_kernel(const float* __restrict__ x,
+                                                                   const int* __restrict__ targets, int64_t rows,
+                                                                   int64_t len, float* __restrict__ stats,
+                                                                   double* __restrict__ part, float* __restrict__ loss) {
+    __shared__ double wave_terms[kRowsPerBlock];
+    const int lane = threadIdx.x % kWave, h = lane >> 5;
+    const int64_t wave_id = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
+    const int64_t waves = int64_t(gridDim.x) * kRowsPerBlock;
+    double total = 0.0;  // lanes 0 and 32: their half's terms
+    for (int64_t pair = wave_id; 2 * pair < rows; pair += waves) {
+        const int64_t r = 2 * pair + h;
+        const int64_t rr = r < rows ? r : rows - 1;  // the upper half of a last, odd pair repeats row rows - 1
+        const int t = targets[rr];
+        f4 v[NV];
+        load_half_row<Vec>(v, x + rr * len, len, lane & 31);
+        total += double(finish_half_row<Vec>(v, rr, r < rows, x + rr * len, len, t, lane, stats));
+    }
+    const uint64_t tb = __builtin_bit_cast(uint64_t, total);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(tb)), 32));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(tb >> 32)), 32));
+    const double upper = __builtin_bit_cast(double, uint64_t(lo) | (uint64_t(hi) << 32));
+    if (lane == 0) wave_terms[threadIdx.x / kWave] = total + upper;
+    finish_loss(wave_terms, part, rows, loss);
 }
 
 // One wavefront per row, streaming the row twice (rows too long for
@@ -579,9 +780,10 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         const bool vec = C % 4 == 0 && aligned16(logits);
         const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
         Profiled p("xent_forward", 0.0, 4.0 * double(R * C) + 4.0 * double(R) + 8.0 * double(R));
-        // Rows of up to 4096 classes are held in registers (NV float4 per lane),
-        // with at most 8 workgroups per CU walking the rows (6 fit at once at
-        // this kernel's register use; 3 to 12 per CU measured within 3%).
+        // Rows are held in registers: up to 1024 classes two rows per wavefront,
+        // up to 4096 one row per wavefront (NV float4 per lane); at most 8
+        // workgroups per CU walk the rows (3 to 12 per CU measured within 3%).
+        // Longer rows are streamed.
         const int64_t nv = (C + kWave * 4 - 1) / (kWave * 4);
         const unsigned cached_grid = unsigned(std::min<int64_t>(
             {(R + kRowsPerBlock - 1) / kRowsPerBlock, int64_t(d.cu_count) * kXentBlocksPerCu,
@@ -589,7 +791,21 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         int64_t blocks = 0;  // loss partials of the streaming path, one double each
         Scratch part(size_t(std::max<int64_t>(cached_grid, (R + red::sum_chunk(R) - 1) / red::sum_chunk(R))) *
                      sizeof(double));
-        if (nv > 16) {
+        const int64_t nh = (C + 127) / 128;  // float4s per lane with a half-wave per row
+        if (nh <= 8) {
+            // Rows of at most 1024 classes: two per wavefront.
+            const unsigned half_grid = unsigned(std::min<int64_t>(
+                {(R + 2 * kRowsPerBlock - 1) / (2 * kRowsPerBlock), int64_t(d.cu_count) * kXentBlocksPerCu,
+                 int64_t(kDoneGroup) * kDoneGroups}));
+#define VC_XENT_HALF(NV)                                                                                        \
+    launch(vec ? xent_half_rows_kernel<NV, true> : xent_half_rows_kernel<NV, false>, dim3(half_grid), dim3(kBlock), \
+           0, d.stream, logits, targets, R, C, row_stats, part.as<double>(), loss)
+            if (nh <= 1) VC_XENT_HALF(1);
+            else if (nh <= 2) VC_XENT_HALF(2);
+            else if (nh <= 4) VC_XENT_HALF(4);
+            else VC_XENT_HALF(8);
+#undef VC_XENT_HALF
+        } else if (nv > 16) {
             // Row terms, then the shared deterministic two-stage sum.
             launch((vec ? xent_rows_kernel<true> : xent_rows_kernel<false>), dim3(grid), dim3(kBlock), 0, d.stream,
                    logits, targets, R, C, row_stats, terms.as<float>());
@@ -607,10 +823,7 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
 #define VC_XENT_ROWS(NV)                                                                                          \
     launch(vec ? xent_rows_cached_kernel<NV, true> : xent_rows_cached_kernel<NV, false>, dim3(cached_grid),     \
            dim3(kBlock), 0, d.stream, logits, targets, R, C, row_stats, part.as<double>(), loss)
-            if (nv <= 1) VC_XENT_ROWS(1);
-            else if (nv <= 2) VC_XENT_ROWS(2);
-            else if (nv <= 4) VC_XENT_ROWS(4);
-            else if (nv <= 8) VC_XENT_ROWS(8);
+            if (nv <= 8) VC_XENT_ROWS(8);  // rows of more than 1024 classes: nv >= 5
             else VC_XENT_ROWS(16);
 #undef VC_XENT_ROWS
         }

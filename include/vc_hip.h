@@ -274,7 +274,7 @@ int vc_hip_reduce_axis(const float* in, float* out, size_t outer, size_t length,
  * is for callers that cannot allocate device memory (code recorded into a HIP
  * graph, tight serving loops, harnesses that forbid allocation). 2 MiB holds
  * the column sums of up to 2^17 outputs (a [8192, 4096] bias gradient needs
- * 256 KiB) and the max/argmax splits of long axes with few outputs; a call that
+ * 1 MiB) and the max/argmax splits of long axes with few outputs; a call that
  * needs more fails with VC_HIP_ERR_INVALID_ARGUMENT before launching
  * anything. Row and one-thread-per-output reductions need no partial results.
  * Calls are serialised

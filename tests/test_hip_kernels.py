@@ -56,13 +56,15 @@ def test_gemm_matches_reference_fixture(golden, gemm_kernel, m, k, n):
                                        err_msg=f"trans_a={ta} trans_b={tb}")
 
 
-# Every shape but the last is above the tiny-product threshold (2^20
-# multiply-adds with K <= 128), so with "mfma" it runs on the MFMA kernel:
+# The first nine shapes are above the small-product threshold (2^20
+# multiply-adds with K <= 1024), so with "mfma" they run on the MFMA kernel:
 # a whole tile, a partial K slice (60, 129), partial m and n tiles (130, 70,
 # 257, 383), and vector and scalar loads in all four transposes. The last
-# runs on the FMA kernel with either setting.
+# three run on the FMA kernel with either setting: K in one slice (7), and
+# K over two and four of its 256-deep slices (300, 1000), the last partial.
 @pytest.mark.parametrize("m,k,n", [(256, 64, 128), (192, 256, 64), (256, 60, 128), (130, 64, 128), (256, 64, 70),
-                                   (257, 129, 383), (512, 1024, 1000), (1, 4096, 3), (2000, 7, 129), (1000, 7, 1)])
+                                   (257, 129, 383), (512, 1024, 1000), (1, 4096, 3), (2000, 7, 129), (1000, 7, 1),
+                                   (64, 300, 3), (2, 1000, 64)])
 def test_gemm_edges_against_oracle(gemm_kernel, m, k, n):
     rng = np.random.default_rng(m * 7 + k * 3 + n)
     for ta in (0, 1):

@@ -54,6 +54,7 @@ constexpr int kGroupM = 8;
 constexpr int64_t kNnViaNtMinRows = VC_NN_VIA_NT_MIN_ROWS;
 constexpr int64_t kTinyTiles = 8;  // outputs of at most this many tiles split K finely
 constexpr double kTinyMacs = 1048576.0;
+constexpr int64_t kSimpleMaxK = 1024;  // and K up to this run on the FMA kernel
 constexpr int kXcds = 8;
 
 struct GemmArgs {
@@ -503,16 +504,71 @@ __global__ __launch_bounds__(256) void transpose64_kernel(const float* __restric
     }
 }
 
-// Portable LDS-tiled FMA kernel (VECTORCORE_HIP_GEMM=simple or
-// vc_hip_set_gemm_kernel("simple"), and tiny products): 16 x 16 outputs
-// per 256-thread workgroup, one per thread.
+// Portable FMA kernel (VECTORCORE_HIP_GEMM=simple or
+// vc_hip_set_gemm_kernel("simple"), and small products): 16 x 16 outputs per
+// 256-thread workgroup, one per thread, each the sum over k in order. K goes
+// through LDS in slices of kSimpleK: each thread issues its share of a slice's
+// loads together (one memory round trip per slice, not per 16 k), and the
+// next slice's loads are in flight while the current slice is summed.
+constexpr int kSimpleK = 256;
+constexpr int kSimpleLoads = 16 * kSimpleK / 256;  // elements of each operand slice per thread
+constexpr int kSimpleAStride = kSimpleK + 4;       // A slice row stride: 16-byte rows for float4 reads
+
+// Thread t's share of a slice, element i (0..15), ordered so that
+// consecutive threads read consecutive addresses of the operand as stored:
+//   A (16 rows x kSimpleK k): stored [M][K]: row i, k t; stored [K][M]: row t % 16, k t / 16 + 16 i;
+//   B (kSimpleK k x 16 columns): stored [K][N]: k t / 16 + 16 i, column t % 16; stored [N][K]: k t, column i.
+// Each operand's 16 addresses step by a fixed stride from one base.
+template <bool TA, bool TB>
+__device__ inline void simple_load(const GemmArgs& p, const float* A, const float* B, int64_t row0, int64_t col0,
+                                   int64_t k0, float (&ra)[kSimpleLoads], float (&rb)[kSimpleLoads]) {
+    const int t = threadIdx.x, lo = t % 16, hi = t / 16;
+    if (TA) {
+        const bool row_ok = row0 + lo < p.M;
+        const float* pa = A + (k0 + hi) * p.lda + row0 + lo;
+        const int64_t step = int64_t(16) * p.lda;
+#pragma unroll
+        for (int i = 0; i < kSimpleLoads; ++i, pa += step) ra[i] = (row_ok && k0 + hi + 16 * i < p.K) ? *pa : 0.0f;
+    } else {
+        const bool k_ok = k0 + t < p.K;
+        const float* pa = A + row0 * p.lda + k0 + t;
+#pragma unroll
+        for (int i = 0; i < kSimpleLoads; ++i, pa += p.lda) ra[i] = (k_ok && row0 + i < p.M) ? *pa : 0.0f;
+    }
+    if (TB) {
+        const bool k_ok = k0 + t < p.K;
+        const float* pb = B + col0 * p.ldb + k0 + t;
+#pragma unroll
+        for (int i = 0; i < kSimpleLoads; ++i, pb += p.ldb) rb[i] = (k_ok && col0 + i < p.N) ? *pb : 0.0f;
+    } else {
+        const bool col_ok = col0 + lo < p.N;
+        const float* pb = B + (k0 + hi) * p.ldb + col0 + lo;
+        const int64_t step = int64_t(16) * p.ldb;
+#pragma unroll
+        for (int i = 0; i < kSimpleLoads; ++i, pb += step) rb[i] = (col_ok && k0 + hi + 16 * i < p.K) ? *pb : 0.0f;
+    }
+}
+
+template <bool TA, bool TB>
+__device__ inline void simple_store(float (*as)[kSimpleAStride], float (*bs)[17], const float (&ra)[kSimpleLoads],
+                                    const float (&rb)[kSimpleLoads]) {
+    const int t = threadIdx.x, lo = t % 16, hi = t / 16;
+#pragma unroll
+    for (int i = 0; i < kSimpleLoads; ++i) {
+        if (TA) as[lo][hi + 16 * i] = ra[i];
+        else as[i][t] = ra[i];
+        if (TB) bs[t][i] = rb[i];
+        else bs[hi + 16 * i][lo] = rb[i];
+    }
+}
+
 template <bool TA, bool TB>
 __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
-    __shared__ float as[16][17];
-    __shared__ float bs[16][17];
+    __shared__ __align__(16) float as[16][kSimpleAStride];
+    __shared__ float bs[kSimpleK][17];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int64_t row = int64_t(blockIdx.x / p.tiles_n) * 16 + ty;
-    const int64_t col = int64_t(blockIdx.x % p.tiles_n) * 16 + tx;
+    const int64_t row0 = int64_t(blockIdx.x / p.tiles_n) * 16, col0 = int64_t(blockIdx.x % p.tiles_n) * 16;
+    const int64_t row = row0 + ty, col = col0 + tx;
     for (int64_t z = blockIdx.y; z < p.batch; z += gridDim.y) {
         const int64_t aoff = p.table ? p.table[2 * z] : z * p.a_bstride;
         const int64_t boff = p.table ? p.table[2 * z + 1] : z * p.b_bstride;
@@ -520,13 +576,32 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
         for (int64_t r = 0; r < p.reduce; ++r) {
             const float* A = p.a + aoff + r * p.a_rstride;
             const float* B = p.b + boff + r * p.b_rstride;
-            for (int64_t k0 = 0; k0 < p.K; k0 += 16) {
-                const int64_t ar = int64_t(blockIdx.x / p.tiles_n) * 16 + ty, ak = k0 + tx;
-                as[ty][tx] = (ar < p.M && ak < p.K) ? (TA ? A[ak * p.lda + ar] : A[ar * p.lda + ak]) : 0.0f;
-                const int64_t bk = k0 + ty, bc = int64_t(blockIdx.x % p.tiles_n) * 16 + tx;
-                bs[ty][tx] = (bk < p.K && bc < p.N) ? (TB ? B[bc * p.ldb + bk] : B[bk * p.ldb + bc]) : 0.0f;
+            float ra[kSimpleLoads], rb[kSimpleLoads];
+            simple_load<TA, TB>(p, A, B, row0, col0, 0, ra, rb);
+            for (int64_t k0 = 0; k0 < p.K; k0 += kSimpleK) {
+                simple_store<TA, TB>(as, bs, ra, rb);
                 __syncthreads();
-                for (int kk = 0; kk < 16; ++kk) acc += as[ty][kk] * bs[kk][tx];
+                if (k0 + kSimpleK < p.K) simple_load<TA, TB>(p, A, B, row0, col0, k0 + kSimpleK, ra, rb);
+                const int kc = int(std::min<int64_t>(kSimpleK, p.K - k0));
+                // Sixteen k per step, every LDS read issued before the first
+                // product, so the reads' latency is paid once per step.
+                int kk = 0;
+                for (; kk + 16 <= kc; kk += 16) {
+                    f4 a4[4];
+                    float b1[16];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) a4[q] = *reinterpret_cast<const f4*>(&as[ty][kk + 4 * q]);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) b1[j] = bs[kk + j][tx];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        acc += a4[q].x * b1[4 * q];
+                        acc += a4[q].y * b1[4 * q + 1];
+                        acc += a4[q].z * b1[4 * q + 2];
+                        acc += a4[q].w * b1[4 * q + 3];
+                    }
+                }
+                for (; kk < kc; ++kk) acc += as[ty][kk] * bs[kk][tx];
                 __syncthreads();
             }
         }
@@ -586,11 +661,12 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     }
     const int64_t tiles_m_simple = (M + 15) / 16, tiles_n_simple = (N + 15) / 16;
     const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    // Tiny products (<= 2^20 multiply-adds, K <= 128) run on the FMA kernel: a
-    // 128 x 128 MFMA tile there is mostly padding, and its fixed latency
-    // (~8 us) is several times the FMA kernel's whole run.
-    const bool simple =
-        force_simple || (double(M) * double(N) * double(K) * double(batch) * double(reduce) <= kTinyMacs && K <= 128);
+    // Small products (<= 2^20 multiply-adds, K <= 1024) run on the FMA kernel:
+    // a 128 x 128 MFMA tile there is mostly padding, and its fixed latency
+    // (~8 us, plus a second pass when K is split) is several times the FMA
+    // kernel's whole run (one memory round trip per 256 k).
+    const bool simple = force_simple || (double(M) * double(N) * double(K) * double(batch) * double(reduce) <=
+                                             kTinyMacs && K <= kSimpleMaxK);
     const int64_t tiles = simple ? tiles_m_simple * tiles_n_simple : tiles_m * tiles_n;
     if (tiles > std::numeric_limits<int>::max() / 2) fail(VC_HIP_ERR_OVERFLOW, "matmul output has too many tiles");
     // Byte offsets relative to a tile origin are 32-bit: 128 rows of any

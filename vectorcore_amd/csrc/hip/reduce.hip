@@ -663,8 +663,9 @@ void reduce_axis(const float* in, float* out, int64_t outer, int64_t len, int64_
 // copy until the process ends. On the host, `scratch` names a stand-in, not
 // device memory: host code uses only the address that hipGetSymbolAddress
 // returns for the current device. A column sum keeps segs * outputs at most
-// 512 * 64 + outputs (double partials), so 2 MiB holds the column sums of up
-// to 2^17 outputs: the bias gradient of a [8192, 4096] layer needs 256 KiB. A
+// 2048 * 64 + outputs double partials (one launch; 512 * 64 + outputs with a
+// separate combine), so 2 MiB holds the column sums of up to 2^17 outputs:
+// the bias gradient of a [8192, 4096] layer needs 1 MiB (32 segments). A
 // max/argmax split over a long axis with few outputs needs 8 bytes per
 // (segment, output); a shape that needs more than the array is rejected.
 constexpr size_t kNoAllocScratchBytes = size_t(2) << 20;

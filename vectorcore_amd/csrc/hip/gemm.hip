@@ -507,65 +507,76 @@ __global__ __launch_bounds__(256) void transpose64_kernel(const float* __restric
 // Portable FMA kernel (VECTORCORE_HIP_GEMM=simple or
 // vc_hip_set_gemm_kernel("simple"), and small products): 16 x 16 outputs per
 // 256-thread workgroup, one per thread, each the sum over k in order. K goes
-// through LDS in slices of kSimpleK: each thread issues its share of a slice's
-// loads together (one memory round trip per slice, not per 16 k), and the
-// next slice's loads are in flight while the current slice is summed.
-constexpr int kSimpleK = 256;
-constexpr int kSimpleLoads = 16 * kSimpleK / 256;  // elements of each operand slice per thread
-constexpr int kSimpleAStride = kSimpleK + 4;       // A slice row stride: 16-byte rows for float4 reads
+// through LDS in slices of KS (16, 64 or 256, the smallest that holds K, up
+// to 256): each thread issues its share of a slice's loads together (one
+// memory round trip per slice), and the next slice's loads are in flight
+// while the current slice is summed.
+//
+// Thread t's share of a slice, element i (0 .. KS / 16 - 1), ordered so that
+// consecutive threads read consecutive addresses of the operand as stored
+// (R = 256 / KS):
+//   A, 16 rows x KS: stored [M][K]: row t / KS + R i, k t % KS; stored [K][M]: row t % 16, k t / 16 + 16 i;
+//   B, KS x 16 columns: stored [K][N]: k t / 16 + 16 i, column t % 16; stored [N][K]: k t % KS, column t / KS + R i.
+// Only elements inside the operand are read; the rest of the slice is 0.
+template <int KS>
+struct SimpleSlice {
+    static constexpr int kLoads = KS / 16;  // elements of each operand per thread
+    static constexpr int kStep = 256 / KS;  // rows (columns) between a thread's elements, [M][K] A and [N][K] B
+    static constexpr int kAStride = KS + 4; // A slice row stride: 16-byte rows for float4 reads
+};
 
-// Thread t's share of a slice, element i (0..15), ordered so that
-// consecutive threads read consecutive addresses of the operand as stored:
-//   A (16 rows x kSimpleK k): stored [M][K]: row i, k t; stored [K][M]: row t % 16, k t / 16 + 16 i;
-//   B (kSimpleK k x 16 columns): stored [K][N]: k t / 16 + 16 i, column t % 16; stored [N][K]: k t, column i.
-// Each operand's 16 addresses step by a fixed stride from one base.
-template <bool TA, bool TB>
+template <bool TA, bool TB, int KS>
 __device__ inline void simple_load(const GemmArgs& p, const float* A, const float* B, int64_t row0, int64_t col0,
-                                   int64_t k0, float (&ra)[kSimpleLoads], float (&rb)[kSimpleLoads]) {
+                                   int64_t k0, float (&ra)[KS / 16], float (&rb)[KS / 16]) {
+    using S = SimpleSlice<KS>;
     const int t = threadIdx.x, lo = t % 16, hi = t / 16;
     if (TA) {
         const bool row_ok = row0 + lo < p.M;
-        const float* pa = A + (k0 + hi) * p.lda + row0 + lo;
-        const int64_t step = int64_t(16) * p.lda;
+        const int64_t base = (k0 + hi) * p.lda + row0 + lo, step = int64_t(16) * p.lda;
 #pragma unroll
-        for (int i = 0; i < kSimpleLoads; ++i, pa += step) ra[i] = (row_ok && k0 + hi + 16 * i < p.K) ? *pa : 0.0f;
+        for (int i = 0; i < S::kLoads; ++i)
+            ra[i] = (row_ok && k0 + hi + 16 * i < p.K) ? A[base + i * step] : 0.0f;
     } else {
-        const bool k_ok = k0 + t < p.K;
-        const float* pa = A + row0 * p.lda + k0 + t;
+        const int64_t k = k0 + t % KS, r = row0 + t / KS;
+        const int64_t base = r * p.lda + k, step = int64_t(S::kStep) * p.lda;
 #pragma unroll
-        for (int i = 0; i < kSimpleLoads; ++i, pa += p.lda) ra[i] = (k_ok && row0 + i < p.M) ? *pa : 0.0f;
+        for (int i = 0; i < S::kLoads; ++i)
+            ra[i] = (k < p.K && r + S::kStep * i < p.M) ? A[base + i * step] : 0.0f;
     }
     if (TB) {
-        const bool k_ok = k0 + t < p.K;
-        const float* pb = B + col0 * p.ldb + k0 + t;
+        const int64_t k = k0 + t % KS, c = col0 + t / KS;
+        const int64_t base = c * p.ldb + k, step = int64_t(S::kStep) * p.ldb;
 #pragma unroll
-        for (int i = 0; i < kSimpleLoads; ++i, pb += p.ldb) rb[i] = (k_ok && col0 + i < p.N) ? *pb : 0.0f;
+        for (int i = 0; i < S::kLoads; ++i)
+            rb[i] = (k < p.K && c + S::kStep * i < p.N) ? B[base + i * step] : 0.0f;
     } else {
         const bool col_ok = col0 + lo < p.N;
-        const float* pb = B + (k0 + hi) * p.ldb + col0 + lo;
-        const int64_t step = int64_t(16) * p.ldb;
+        const int64_t base = (k0 + hi) * p.ldb + col0 + lo, step = int64_t(16) * p.ldb;
 #pragma unroll
-        for (int i = 0; i < kSimpleLoads; ++i, pb += step) rb[i] = (col_ok && k0 + hi + 16 * i < p.K) ? *pb : 0.0f;
+        for (int i = 0; i < S::kLoads; ++i)
+            rb[i] = (col_ok && k0 + hi + 16 * i < p.K) ? B[base + i * step] : 0.0f;
     }
 }
 
-template <bool TA, bool TB>
-__device__ inline void simple_store(float (*as)[kSimpleAStride], float (*bs)[17], const float (&ra)[kSimpleLoads],
-                                    const float (&rb)[kSimpleLoads]) {
+template <bool TA, bool TB, int KS>
+__device__ inline void simple_store(float (*as)[SimpleSlice<KS>::kAStride], float (*bs)[17], const float (&ra)[KS / 16],
+                                    const float (&rb)[KS / 16]) {
+    using S = SimpleSlice<KS>;
     const int t = threadIdx.x, lo = t % 16, hi = t / 16;
 #pragma unroll
-    for (int i = 0; i < kSimpleLoads; ++i) {
+    for (int i = 0; i < S::kLoads; ++i) {
         if (TA) as[lo][hi + 16 * i] = ra[i];
-        else as[i][t] = ra[i];
-        if (TB) bs[t][i] = rb[i];
+        else as[t / KS + S::kStep * i][t % KS] = ra[i];
+        if (TB) bs[t % KS][t / KS + S::kStep * i] = rb[i];
         else bs[hi + 16 * i][lo] = rb[i];
     }
 }
 
-template <bool TA, bool TB>
+template <bool TA, bool TB, int KS>
 __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
-    __shared__ __align__(16) float as[16][kSimpleAStride];
-    __shared__ float bs[kSimpleK][17];
+    using S = SimpleSlice<KS>;
+    __shared__ __align__(16) float as[16][S::kAStride];
+    __shared__ float bs[KS][17];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     const int64_t row0 = int64_t(blockIdx.x / p.tiles_n) * 16, col0 = int64_t(blockIdx.x % p.tiles_n) * 16;
     const int64_t row = row0 + ty, col = col0 + tx;
@@ -576,15 +587,15 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
         for (int64_t r = 0; r < p.reduce; ++r) {
             const float* A = p.a + aoff + r * p.a_rstride;
             const float* B = p.b + boff + r * p.b_rstride;
-            float ra[kSimpleLoads], rb[kSimpleLoads];
-            simple_load<TA, TB>(p, A, B, row0, col0, 0, ra, rb);
-            for (int64_t k0 = 0; k0 < p.K; k0 += kSimpleK) {
-                simple_store<TA, TB>(as, bs, ra, rb);
+            float ra[S::kLoads], rb[S::kLoads];
+            simple_load<TA, TB, KS>(p, A, B, row0, col0, 0, ra, rb);
+            for (int64_t k0 = 0; k0 < p.K; k0 += KS) {
+                simple_store<TA, TB, KS>(as, bs, ra, rb);
                 __syncthreads();
-                if (k0 + kSimpleK < p.K) simple_load<TA, TB>(p, A, B, row0, col0, k0 + kSimpleK, ra, rb);
-                const int kc = int(std::min<int64_t>(kSimpleK, p.K - k0));
+                if (k0 + KS < p.K) simple_load<TA, TB, KS>(p, A, B, row0, col0, k0 + KS, ra, rb);
                 // Sixteen k per step, every LDS read issued before the first
                 // product, so the reads' latency is paid once per step.
+                const int kc = int(std::min<int64_t>(KS, p.K - k0));
                 int kk = 0;
                 for (; kk + 16 <= kc; kk += 16) {
                     f4 a4[4];
@@ -617,7 +628,9 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
 template <bool TA, bool TB>
 void launch_variant(const GemmArgs& args, bool vec, bool simple, dim3 grid, hipStream_t stream) {
     if (simple) {
-        launch((gemm_simple_kernel<TA, TB>), grid, dim3(256), 0, stream, args);
+        if (args.K <= 16) launch((gemm_simple_kernel<TA, TB, 16>), grid, dim3(256), 0, stream, args);
+        else if (args.K <= 64) launch((gemm_simple_kernel<TA, TB, 64>), grid, dim3(256), 0, stream, args);
+        else launch((gemm_simple_kernel<TA, TB, 256>), grid, dim3(256), 0, stream, args);
     } else if (vec) {
         launch((gemm_mfma_kernel<TA, TB, true>), grid, dim3(kThreads), 0, stream, args);
     } else {

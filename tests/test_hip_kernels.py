@@ -444,7 +444,12 @@ def test_cross_entropy_matches_reference_fixture(golden):
     np.testing.assert_allclose(grad, golden["xent_grad"], rtol=1e-5, atol=1e-9)
 
 
-@pytest.mark.parametrize("rows,classes", [(512, 1000), (300, 3), (64, 37), (4, 2)])
+# Two rows per wavefront hold 1, 2, 4 or 8 float4s per lane (up to 128, 256,
+# 512, 1024 classes): 3, 37, 2 and 130 (scalar loads), 200 and 512 (vector
+# loads, 200 a partial last float4 slot), 257 and 1000; odd row counts leave
+# the last wavefront half a pair.
+@pytest.mark.parametrize("rows,classes", [(512, 1000), (300, 3), (64, 37), (4, 2), (257, 200), (65, 130),
+                                          (33, 512), (31, 257)])
 def test_cross_entropy_against_oracle(rows, classes):
     from oracle import autograd as A
     xe = W.xent(rows=rows, classes=classes, seed=rows + classes)
@@ -566,11 +571,12 @@ def _special_rows(classes, rng):
     return np.stack(rows), targets
 
 
-@pytest.mark.parametrize("classes", [1000, 40, 37, 2000, 4100])
+@pytest.mark.parametrize("classes", [1000, 40, 37, 200, 510, 2000, 4100])
 def test_cross_entropy_special_values_match_the_oracle(classes):
-    # 1000 and 40 take the register-held kernel with two rows per wavefront,
-    # 37 (not a multiple of 4) the same kernel with scalar loads and a partial
-    # last float4, 2000 the kernel with one row per wavefront, 4100 (too long
+    # 1000, 40 and 200 take the register-held kernel with two rows per
+    # wavefront (8, 1 and 2 float4s per lane), 37 and 510 (not multiples of 4)
+    # the same kernel with scalar loads and a partial last float4 (1 and 4
+    # per lane), 2000 the kernel with one row per wavefront, 4100 (too long
     # for registers) the streaming one. Each row alone, so
     # one NaN row does not hide the others; the row maximum must carry the
     # reference's sign of zero.

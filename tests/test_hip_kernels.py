@@ -522,13 +522,14 @@ def test_cross_entropy_vector_and_scalar_loads_agree(classes):
 
 
 @pytest.mark.parametrize("rows,classes", [(8192, 1000), (17, 1000), (300, 37), (300, 3), (100, 3000), (64, 2048),
-                                          (5, 4)])
+                                          (5, 4), (300, 500), (33, 301)])
 def test_cross_entropy_backward_with_column_sums(rows, classes):
     """vc_hip_xent_backward_colsum: the gradient is the plain backward's bits
-    and the column sums equal the oracle's reduction of that gradient. 37
-    classes (not a multiple of 4) load the rows with scalar loads, 3000
+    and the column sums equal the oracle's reduction of that gradient. The
+    rows take 1, 2, 4 or 8 float4s per lane (3, 500, 1000, 2048 classes); 37
+    and 301 classes (not multiples of 4) load the rows with scalar loads, 3000
     (beyond the register-held rows) takes the plain kernel and a separate
-    reduction; 17 rows leave the last row block short."""
+    reduction; 17 and 33 rows leave the last row block short."""
     xe = W.xent(rows=rows, classes=classes, seed=rows + classes)
     logits, targets = xe["logits"], xe["targets"].astype(np.int32)
     dl, dt = C.Buffer.of(logits), C.Buffer.of(targets, dtype=np.int32)

@@ -723,20 +723,16 @@ int vc_hip_reduce_sum(const float* in, size_t count, float* out) {
         if (!out) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_reduce_sum: null output");
         const int64_t n = int64_t(count);
         const int64_t chunk = red::sum_chunk(n);
-        const int64_t blocks = n == 0 ? 0 : (n + chunk - 1) / chunk;
-        Scratch part(size_t(std::max<int64_t>(blocks, 1)) * sizeof(double));
+        // One launch: at most 2048 chunks (sum_chunk), at least one block.
+        const int64_t blocks = std::max<int64_t>(1, (n + chunk - 1) / chunk);
+        Scratch part(size_t(blocks) * sizeof(double));
         Profiled p("reduce_sum", double(n), 4.0 * double(n));
-        if (blocks > 0) {
-            if (aligned16(in))
-                launch(red::sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, in,
-                                   part.as<double>(), n, chunk);
-            else
-                launch(red::sum_partial_kernel<false>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, in,
-                                   part.as<double>(), n, chunk);
-            after_launch("reduce_sum");
-        }
-        launch(red::sum_final_kernel<red::Identity>, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), out,
-                           blocks, red::Identity());
+        if (aligned16(in))
+            launch(red::sum_finish_kernel<true, red::Identity>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, in,
+                   part.as<double>(), out, n, chunk, red::Identity());
+        else
+            launch(red::sum_finish_kernel<false, red::Identity>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream,
+                   in, part.as<double>(), out, n, chunk, red::Identity());
         after_launch("reduce_sum");
         p.done();
     });

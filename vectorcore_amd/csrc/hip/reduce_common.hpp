@@ -1,7 +1,8 @@
 // Device helpers shared by the reduction and cross-entropy kernels:
 // wavefront/workgroup double sums with a fixed combine order, the first
-// strict maximum of a row, and the two-stage full sum (fixed chunks, then one
-// workgroup).
+// strict maximum of a row, the one-launch finish (the block that finishes last
+// adds the blocks' partials) and the full sum (fixed chunks, then their sum in
+// a fixed order, in one launch or two).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -179,6 +180,70 @@ __device__ inline double chunk_sum(const float* __restrict__ x, int64_t b0, int6
     return acc;
 }
 
+// ---- one launch: the block that finishes last adds the partials -----------
+// Each block writes its partial with a device-scope store, waits for it to
+// complete (s_waitcnt 0: a device-scope store is acknowledged once it is
+// visible at device scope, so no release fence, and no L2 writeback, is
+// needed), then counts itself in on its group's device-scope counter (groups
+// of kDoneGroup blocks, one counter per 128-byte line, so the count is not one
+// long queue on one address). The block that completes a group resets that
+// counter and counts the group in on the top counter; the block that
+// completes the last group reads every partial with device-scope loads and
+// adds them as sum_final_kernel does (thread t takes blocks t, t + 256, ...,
+// then the fixed workgroup tree), so the result does not depend on which
+// block is last, and it resets the top counter for the next launch. Launches
+// on the library's one stream never overlap, so each translation unit's
+// counters (static, zero at load) serve all its one-launch kernels.
+constexpr unsigned kDoneGroup = 64, kDoneGroups = 64, kDoneStride = 32;
+constexpr unsigned kMaxFinishBlocks = kDoneGroup * kDoneGroups;
+static __device__ unsigned int g_group_done[kDoneGroups * kDoneStride];
+static __device__ unsigned int g_groups_done;
+
+// Thread 0 holds the block's partial; every thread of the block learns
+// whether it finished last. Grids of at most kMaxFinishBlocks blocks.
+__device__ inline bool count_in(double block_partial, double* __restrict__ part) {
+    __shared__ int last_block;
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(&part[blockIdx.x], block_partial, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        const unsigned group = blockIdx.x / kDoneGroup, groups = (gridDim.x + kDoneGroup - 1) / kDoneGroup;
+        const unsigned members = min(kDoneGroup, gridDim.x - group * kDoneGroup);
+        unsigned* counter = &g_group_done[group * kDoneStride];
+        bool last = false;
+        if (__hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == members) {
+            __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            last = __hip_atomic_fetch_add(&g_groups_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == groups;
+        }
+        last_block = last;
+    }
+    __syncthreads();
+    return last_block;
+}
+
+// In the block that finished last: the sum of part[0, gridDim.x), valid in
+// thread 0, which also resets the top counter. Device-scope (cache policy
+// sc1 = 16) loads, eight in flight per thread.
+__device__ inline double finish_partials(const double* __restrict__ part, double* lds) {
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<double*>(part), short(0), int(gridDim.x * sizeof(double)), 0x00020000);
+    double acc = 0.0;
+    for (unsigned b0 = threadIdx.x; b0 < gridDim.x; b0 += 8 * blockDim.x) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const unsigned b = b0 + u * blockDim.x;  // past the grid: outside the descriptor, reads 0 (not added)
+            v[u] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rp, b * 8u, 0, 16));
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (b0 + u * blockDim.x < gridDim.x) acc += v[u];
+    }
+    const double total = block_sum(acc, lds);
+    if (threadIdx.x == 0) __hip_atomic_store(&g_groups_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return total;
+}
+
 // Stage one: part[b] = sum of x[b*chunk, (b+1)*chunk) in double.
 template <bool Vec>
 __global__ __launch_bounds__(kBlock) void sum_partial_kernel(const float* __restrict__ x, double* __restrict__ part,
@@ -187,6 +252,21 @@ __global__ __launch_bounds__(kBlock) void sum_partial_kernel(const float* __rest
     const int64_t b0 = int64_t(blockIdx.x) * chunk, b1 = b0 + chunk < n ? b0 + chunk : n;
     const double total = block_sum(chunk_sum<Vec>(x, b0, b1), lds);
     if (threadIdx.x == 0) part[blockIdx.x] = total;
+}
+
+// Both stages in one launch (grids of at most kMaxFinishBlocks chunks, and at
+// least one block: an empty input sums to 0): the same partials, added in the
+// same order as sum_final_kernel, by the block that finishes last.
+template <bool Vec, class Finish>
+__global__ __launch_bounds__(kBlock) void sum_finish_kernel(const float* __restrict__ x, double* __restrict__ part,
+                                                            float* __restrict__ out, int64_t n, int64_t chunk,
+                                                            Finish finish) {
+    __shared__ double lds[kBlock / kWave];
+    const int64_t b0 = int64_t(blockIdx.x) * chunk, b1 = b0 + chunk < n ? b0 + chunk : n;
+    const double partial = block_sum(chunk_sum<Vec>(x, b0, b1), lds);
+    if (!count_in(partial, part)) return;
+    const double total = finish_partials(part, lds);
+    if (threadIdx.x == 0) out[0] = finish(float(total));
 }
 
 // Stage two: out = finish(float(sum of the partials)); thread t takes

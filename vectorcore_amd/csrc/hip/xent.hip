@@ -265,19 +265,8 @@ __device__ inline void load_row(f4 (&v)[NV], const float* __restrict__ row, int6
 // then the block's wavefronts in order, into one double per block.
 //
 // The block that finishes last also finishes the loss, so the forward is one
-// launch: each block writes its partial with a device-scope store, waits for
-// it to complete, then counts itself in on its group's device-scope counter
-// (groups of kDoneGroup blocks, one counter per 128-byte line, so the count
-// is not one long queue on one address); the block that completes a group
-// resets that counter and counts the group in on the top counter. The block
-// that completes the last group reads every partial with device-scope loads
-// and adds them as sum_final_kernel does (thread t takes blocks t, t + 256,
-// ..., then the fixed workgroup tree), so the loss does not depend on which
-// block is last, and resets the top counter for the next launch (launches on
-// the library's one stream never overlap).
-constexpr unsigned kDoneGroup = 64, kDoneGroups = 64, kDoneStride = 32;
-__device__ unsigned int g_xent_group_done[kDoneGroups * kDoneStride];
-__device__ unsigned int g_xent_groups_done;
+// launch (red::count_in and red::finish_partials: the partials are added in
+// block order whichever block is last).
 
 // ---- two rows per wavefront: lanes 0-31 hold one row, lanes 32-63 the next --
 // For rows of at most 1024 classes. A row's cross-lane reductions then take
@@ -447,59 +436,20 @@ struct NegateDivide {
 };
 
 // The end of a one-launch forward: each wavefront's loss terms are in
-// wave_terms. Block b adds them in wave order into part[b] with a
-// device-scope store, waits for it, and counts itself in on its group's
-// counter; the block completing a group counts the group in on the top
-// counter, and the block completing the last group adds all partials in
-// block order, writes the loss and resets the counters.
+// wave_terms. Block b adds them in wave order into its partial; the block
+// that finishes last adds all partials in block order (red::count_in,
+// red::finish_partials) and writes the loss.
 __device__ inline void finish_loss(double* wave_terms, double* __restrict__ part, int64_t rows,
                                    float* __restrict__ loss) {
-    __shared__ int last_block;
     __syncthreads();
+    double sum = 0.0;
     if (threadIdx.x == 0) {
-        double sum = wave_terms[0];
+        sum = wave_terms[0];
         for (int w = 1; w < kRowsPerBlock; ++w) sum += wave_terms[w];
-        __hip_atomic_store(&part[blockIdx.x], sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // A device-scope store is acknowledged once it is visible at device
-        // scope; waiting for every outstanding memory operation (vmcnt 0)
-        // therefore orders it before the count below. (A release fence would
-        // also write back the whole L2, which this store does not need.)
-        __builtin_amdgcn_s_waitcnt(0);
-        const unsigned group = blockIdx.x / kDoneGroup, groups = (gridDim.x + kDoneGroup - 1) / kDoneGroup;
-        const unsigned members = min(kDoneGroup, gridDim.x - group * kDoneGroup);
-        unsigned* counter = &g_xent_group_done[group * kDoneStride];
-        bool last = false;
-        if (__hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == members) {
-            __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_s_waitcnt(0);
-            last = __hip_atomic_fetch_add(&g_xent_groups_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
-                   groups;
-        }
-        last_block = last;
     }
-    __syncthreads();
-    if (!last_block) return;
-    // Device-scope loads (cache policy sc1 = 16), eight in flight per thread,
-    // then added in block order.
-    const __amdgpu_buffer_rsrc_t rp =
-        __builtin_amdgcn_make_buffer_rsrc(part, short(0), int(gridDim.x * sizeof(double)), 0x00020000);
-    double acc = 0.0;
-    for (unsigned b0 = threadIdx.x; b0 < gridDim.x; b0 += 8 * blockDim.x) {
-        double v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const unsigned b = b0 + u * blockDim.x;  // past the grid: outside the descriptor, reads 0 (not added)
-            v[u] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rp, b * 8u, 0, 16));
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (b0 + u * blockDim.x < gridDim.x) acc += v[u];
-    }
-    const double sum = red::block_sum(acc, wave_terms);
-    if (threadIdx.x == 0) {
-        loss[0] = NegateDivide{float(rows)}(float(sum));
-        __hip_atomic_store(&g_xent_groups_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (!red::count_in(sum, part)) return;
+    const double total = red::finish_partials(part, wave_terms);
+    if (threadIdx.x == 0) loss[0] = NegateDivide{float(rows)}(float(total));
 }
 
 template <int NV, bool Vec>
@@ -787,8 +737,7 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
         const int64_t nv = (C + kWave * 4 - 1) / (kWave * 4);
         const unsigned cached_grid = unsigned(std::min<int64_t>(
             {(R + kRowsPerBlock - 1) / kRowsPerBlock, int64_t(d.cu_count) * kXentBlocksPerCu,
-             int64_t(kDoneGroup) * kDoneGroups}));
-        int64_t blocks = 0;  // loss partials of the streaming path, one double each
+             int64_t(red::kMaxFinishBlocks)}));
         Scratch part(size_t(std::max<int64_t>(cached_grid, (R + red::sum_chunk(R) - 1) / red::sum_chunk(R))) *
                      sizeof(double));
         const int64_t nh = (C + 127) / 128;  // float4s per lane with a half-wave per row
@@ -796,7 +745,7 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
             // Rows of at most 1024 classes: two per wavefront.
             const unsigned half_grid = unsigned(std::min<int64_t>(
                 {(R + 2 * kRowsPerBlock - 1) / (2 * kRowsPerBlock), int64_t(d.cu_count) * kXentBlocksPerCu,
-                 int64_t(kDoneGroup) * kDoneGroups}));
+                 int64_t(red::kMaxFinishBlocks)}));
 #define VC_XENT_HALF(NV)                                                                                        \
     launch(vec ? xent_half_rows_kernel<NV, true> : xent_half_rows_kernel<NV, false>, dim3(half_grid), dim3(kBlock), \
            0, d.stream, logits, targets, R, C, row_stats, part.as<double>(), loss)
@@ -806,17 +755,14 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
             else VC_XENT_HALF(8);
 #undef VC_XENT_HALF
         } else if (nv > 16) {
-            // Row terms, then the shared deterministic two-stage sum.
+            // Row terms, then the shared deterministic full sum (one launch).
             launch((vec ? xent_rows_kernel<true> : xent_rows_kernel<false>), dim3(grid), dim3(kBlock), 0, d.stream,
                    logits, targets, R, C, row_stats, terms.as<float>());
             after_launch("xent_forward");
             const int64_t chunk = red::sum_chunk(R);
-            blocks = (R + chunk - 1) / chunk;
-            launch(red::sum_partial_kernel<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream,
-                   terms.as<float>(), part.as<double>(), R, chunk);
-            after_launch("xent_forward");
-            launch(red::sum_final_kernel<NegateDivide>, dim3(1), dim3(kBlock), 0, d.stream, part.as<double>(), loss,
-                   blocks, NegateDivide{float(R)});
+            const int64_t blocks = (R + chunk - 1) / chunk;
+            launch(red::sum_finish_kernel<true, NegateDivide>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream,
+                   terms.as<float>(), part.as<double>(), loss, R, chunk, NegateDivide{float(R)});
         } else {
             // Register-held rows; the row kernel sums the terms per block and
             // its last block finishes the loss.

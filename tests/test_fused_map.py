@@ -115,7 +115,10 @@ def test_random_programs_bitexact(rows, cols, offset, seed):
         assert_same_values(g, want[s])
 
 
-@pytest.mark.parametrize("rows,cols", [(4096, 4096), (1000, 256), (37, 1000), (50, 130), (3, 64), (1, 5), (9, 1)])
+# Vector and scalar loads, one to 2048 partial rows per column, and a row
+# too wide for one column block's partial row count to matter (2, 300001).
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (1000, 256), (37, 1000), (50, 130), (3, 64), (1, 5), (9, 1),
+                                       (4000, 130), (2, 300001)])
 def test_column_sums(rows, cols):
     rng = np.random.default_rng(rows * 7 + cols)
     inputs = [rng.standard_normal((rows, cols)).astype(np.float32) for _ in range(3)]

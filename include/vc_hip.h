@@ -277,9 +277,10 @@ int vc_hip_reduce_axis(const float* in, float* out, size_t outer, size_t length,
  * 1 MiB) and the max/argmax splits of long axes with few outputs; a call that
  * needs more fails with VC_HIP_ERR_INVALID_ARGUMENT before launching
  * anything. Row and one-thread-per-output reductions need no partial results.
- * Calls are serialised
- * by the library and run in order on its one stream, so consecutive calls
- * reuse the array safely; nothing in it needs to start at zero. */
+ * Calls are serialised by the library and run in order on its one stream, so
+ * consecutive calls reuse the array safely; nothing in it needs to start at
+ * zero. Work that overlaps on one GPU (a recorded graph replayed alongside the
+ * library's stream) races on the array and on the completion counters. */
 int vc_hip_reduce_axis_noalloc(const float* in, float* out, size_t outer, size_t length, size_t inner, int op);
 /* MetalBackend::scatter_axis (metal_backend.hpp:49-51). */
 int vc_hip_scatter_axis(const float* values, const float* indices, float* out, size_t outer, size_t length,

@@ -59,3 +59,35 @@ def test_unavailable_device_is_reported_by_status():
     assert lib.vc_hip_synchronize() == 0  # a no-op without a device, as in the reference
     with pytest.raises(RuntimeError, match="unavailable"):
         C.check(lib.vc_hip_fill(None, 4, ctypes.c_float(1.0)))
+
+
+def test_a_c_program_compiles_and_links_against_the_header(tmp_path):
+    # The boundary is plain C: a C99 translation unit that calls every group of
+    # entry points compiles warning-free with the header alone and links
+    # against the built library (nothing runs: no device here).
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "uses_abi.c"
+    src.write_text(
+        '#include "vc_hip.h"\n'
+        "int main(void) {\n"
+        "    vc_hip_map_program program = {0};\n"
+        "    void* p = 0;\n"
+        "    size_t off = 0;\n"
+        "    int status = vc_hip_available() ? 0 : 1;\n"
+        "    status |= vc_hip_alloc(16, &p);\n"
+        "    status |= vc_hip_matmul(0, 0, 0, 1, 1, 1, &off, &off, 1, 0, 0);\n"
+        "    status |= vc_hip_reduce_axis_noalloc(0, 0, 1, 1, 1, VC_REDUCE_SUM);\n"
+        "    status |= vc_hip_map(&program);\n"
+        "    status |= vc_hip_xent_forward(0, 0, 1, 1, 0, 0);\n"
+        "    return status;\n"
+        "}\n")
+    lib = Path(C.LIB_PATH)
+    out = tmp_path / "uses_abi"
+    r = subprocess.run([cc, "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", str(HEADER.parent),
+                        str(src), "-o", str(out), "-L", str(lib.parent), "-lvc_hip", f"-Wl,-rpath,{lib.parent}"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr

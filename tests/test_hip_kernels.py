@@ -410,6 +410,18 @@ def test_reduce_sum_edges():
         np.testing.assert_allclose(s.numpy()[0], K.sum_all(x), rtol=1e-6, atol=1e-6)
 
 
+def test_reduce_sum_one_launch_large_unaligned_and_repeated():
+    # 2^25 + 1 floats: 2048 chunks (the most one launch takes) and a partial
+    # last chunk; read from an address one float past alignment (scalar
+    # loads) and aligned, twice each (the completion counters reset).
+    n = (1 << 25) + 1
+    x = np.random.default_rng(11).standard_normal(n + 1).astype(np.float32)
+    dx, s = C.Buffer.of(x), C.Buffer((1,))
+    for shift in (1, 0, 1, 0):
+        C.check(C.lib().vc_hip_reduce_sum(dx.ptr + 4 * shift, n, s.ptr))
+        np.testing.assert_allclose(s.numpy()[0], K.sum_all(x[shift:shift + n]), rtol=1e-6, atol=1e-4)
+
+
 def test_scatter_and_transpose_exact():
     rng = np.random.default_rng(9)
     x = rng.standard_normal((6, 40, 9)).astype(np.float32)

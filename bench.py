@@ -54,6 +54,33 @@ def copy_calibration_pass(vc):
     vc.synchronize()
 
 
+def mlp_step(vc, m):
+    """One train step of the MLP `m` (workloads.mlp) on the hip device:
+    x @ W + b per layer, ReLU between layers, cross-entropy, backward, SGD,
+    gradients zeroed, the loss read."""
+    params = []
+    for w, b in zip(m["weights"], m["biases"]):
+        params += [vc.Tensor(w, requires_grad=True, device="hip"), vc.Tensor(b, requires_grad=True, device="hip")]
+    x = vc.Tensor(m["x"], device="hip")
+    targets = m["targets"]
+    lr = m["lr"]
+    layers = len(m["weights"])
+
+    def step():
+        h = x
+        for i in range(layers):
+            h = h @ params[2 * i] + params[2 * i + 1]
+            if i < layers - 1:
+                h = h.relu()
+        loss = vc.cross_entropy(h, targets)
+        loss.backward()
+        vc.sgd_step(params, lr)
+        vc.zero_grad(params)
+        return loss.item()
+
+    return step
+
+
 def gpu_bench(steps: int, warmup: int, copy_calibration: bool = False):
     import numpy as np
 
@@ -62,25 +89,7 @@ def gpu_bench(steps: int, warmup: int, copy_calibration: bool = False):
 
     if not vc.hip_available():
         raise SystemExit("bench.py: the hip device is unavailable: the MI355X backend needs a gfx950 GPU")
-    m = W.mlp(batch=BATCH, dims=DIMS)
-    params = []
-    for w, b in zip(m["weights"], m["biases"]):
-        params += [vc.Tensor(w, requires_grad=True, device="hip"), vc.Tensor(b, requires_grad=True, device="hip")]
-    x = vc.Tensor(m["x"], device="hip")
-    targets = m["targets"]
-    lr = m["lr"]
-
-    def step():
-        h = x
-        for i in range(3):
-            h = h @ params[2 * i] + params[2 * i + 1]
-            if i < 2:
-                h = h.relu()
-        loss = vc.cross_entropy(h, targets)
-        loss.backward()
-        vc.sgd_step(params, lr)
-        vc.zero_grad(params)
-        return loss.item()
+    step = mlp_step(vc, W.mlp(batch=BATCH, dims=DIMS))
 
     if copy_calibration:
         copy_calibration_pass(vc)
@@ -328,6 +337,49 @@ def measure_xent(vc, W, ref):
     return c4
 
 
+ONE_HIDDEN_DIMS = (1024, 4096, 1000)
+ONE_HIDDEN_STEPS = 20
+
+
+def measure_mlp_one_hidden(vc, W, ref):
+    """The one-hidden-layer network 8192 x 1024 -> 4096 -> 1000 (the headline
+    runs 1024 -> 4096 -> 4096 -> 1000): the same train step, seed and
+    initialisation; steps/s over ONE_HIDDEN_STEPS steps after 3 warm-up steps,
+    and the backward GEMMs' rate from events on their dispatches."""
+    m = W.mlp(batch=BATCH, dims=ONE_HIDDEN_DIMS)
+    step = mlp_step(vc, m)
+    for _ in range(3):
+        step()
+    vc.synchronize()
+    vc.hip_profile(True, labels=list(BWD_GEMM_LABELS))
+    vc.hip_profile_reset()
+    t0 = time.perf_counter()
+    losses = [step() for _ in range(ONE_HIDDEN_STEPS)]
+    vc.synchronize()
+    elapsed = time.perf_counter() - t0
+    prof = vc.hip_profile_read()
+    vc.hip_profile(False)
+    _, bwd_flops = W.mlp_gemm_flops(BATCH, ONE_HIDDEN_DIMS)
+    gemm_ms = sum(v["ms"] for v in prof.values()) / ONE_HIDDEN_STEPS
+    tflops = bwd_flops / gemm_ms / 1e9
+    out = {"workload": "MLP 1024->4096->1000 fp32 (ReLU), batch 8192: forward, softmax cross-entropy, backward, "
+                       "SGD lr 0.01", "bound": "mfma", "hip_steps_per_s": round(ONE_HIDDEN_STEPS / elapsed, 2),
+           "ms_per_step": round(elapsed * 1e3 / ONE_HIDDEN_STEPS, 3), "bwd_gemm_tflops": round(tflops, 1),
+           "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4), "loss_first_last": [round(losses[0], 5),
+                                                                                round(losses[-1], 5)]}
+    if ref:
+        net = ref.mlp(m["weights"], m["biases"], m["x"], m["targets"])
+        net.step(m["lr"])
+        times = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            net.step(m["lr"])
+            times.append(time.perf_counter() - t0)
+        out["cpu_reference_steps_per_s"] = round(1.0 / min(times), 4)
+        out["cpu_reference_sample"] = "full 8192-row steps: 1 warm-up, then the faster of 2"
+    return out
+
+
 def measure_column_sums(vc):
     """The standalone column-sum reduction (axis-0 sum) on the train step's
     bias-gradient shapes: the kernel a bias gradient takes when its producer
@@ -350,7 +402,7 @@ def measure_column_sums(vc):
 
 
 CONFIGS = ("spiral_train_step", "batched_matmul_backward", "batched_matmul_backward_broadcast_b",
-           "activation_backward", "cross_entropy", "column_sums")
+           "activation_backward", "cross_entropy", "column_sums", "mlp_one_hidden_layer")
 
 
 def config_measurements(cpu: bool, only=None):
@@ -367,6 +419,7 @@ def config_measurements(cpu: bool, only=None):
         "activation_backward": lambda: measure_activation(vc, W, ref),
         "cross_entropy": lambda: measure_xent(vc, W, ref),
         "column_sums": lambda: measure_column_sums(vc),
+        "mlp_one_hidden_layer": lambda: measure_mlp_one_hidden(vc, W, ref),
     }
     out = {}
     for name in (only or CONFIGS):

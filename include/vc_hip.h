@@ -293,6 +293,14 @@ int vc_hip_scatter_axis(const float* values, const float* indices, float* out, s
  * already checked against `classes` by the caller. */
 int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows, size_t classes,
                         float* row_stats, float* loss);
+/* vc_hip_xent_forward followed by vc_hip_mirror_scalar(loss), with one launch
+ * fewer: the forward's own kernel writes the mirror's host slot when it can.
+ * *mirror is then read and released like vc_hip_mirror_scalar's. The fused
+ * loss node of src/nn.cpp:31-53 whose value loss.item() reads; like the
+ * mirrors, no counterpart in the reference's download
+ * (metal_backend.mm:198-211). */
+int vc_hip_xent_forward_published(const float* logits, const int32_t* targets, size_t rows, size_t classes,
+                                  float* row_stats, float* loss, vc_hip_mirror** mirror);
 /* grad_logits = (softmax(logits) - onehot(targets)) * grad_loss[0] / rows,
  * evaluated as the reference's composed backward does. grad_loss is a device
  * scalar (the upstream gradient of the loss). */

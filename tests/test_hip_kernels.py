@@ -637,6 +637,37 @@ def test_scalar_mirror_publishes_the_value_at_its_point_in_the_stream():
     assert C.lib().vc_hip_mirror_scalar(None, ctypes.byref(m)) != 0
 
 
+@pytest.mark.parametrize("rows,classes", [(257, 1000), (64, 2000), (33, 5000), (5, 3)])
+@pytest.mark.parametrize("profiling", [False, True])
+def test_published_forward_matches_the_forward_and_its_mirror(rows, classes, profiling):
+    # vc_hip_xent_forward_published: the loss and statistics bits of
+    # vc_hip_xent_forward, and a mirror holding the loss. Register-held rows
+    # (1000, 2000, 3 classes) write the host slot from the forward's kernel
+    # unless the profiler holds its dispatch events; streamed rows (5000) and
+    # profiled calls publish with a copy after the forward.
+    rng = np.random.default_rng(rows + classes)
+    x = (rng.standard_normal((rows, classes)) * 2).astype(np.float32)
+    t = rng.integers(0, classes, rows).astype(np.int32)
+    dx, dt = C.Buffer.of(x), C.Buffer.of(t, dtype=np.int32)
+    st1, st2 = C.Buffer((rows, 2)), C.Buffer((rows, 2))
+    l1, l2 = C.Buffer((1,)), C.Buffer((1,))
+    C.check(C.lib().vc_hip_xent_forward(dx.ptr, dt.ptr, rows, classes, st1.ptr, l1.ptr))
+    m = ctypes.c_void_p()
+    C.profile(profiling)
+    try:
+        C.check(C.lib().vc_hip_xent_forward_published(dx.ptr, dt.ptr, rows, classes, st2.ptr, l2.ptr, ctypes.byref(m)))
+    finally:
+        C.profile(False)
+    C.check(C.lib().vc_hip_fill(l2.ptr, 1, ctypes.c_float(-7.0)))  # after the published value
+    v = ctypes.c_float()
+    C.check(C.lib().vc_hip_mirror_read(m, ctypes.byref(v)))
+    C.check(C.lib().vc_hip_mirror_release(m))
+    assert np.float32(v.value).tobytes() == l1.numpy()[0].tobytes()
+    np.testing.assert_array_equal(st2.numpy(), st1.numpy())
+    assert l2.numpy()[0] == -7.0
+    assert C.lib().vc_hip_xent_forward_published(dx.ptr, dt.ptr, rows, classes, st2.ptr, l2.ptr, None) != 0
+
+
 def test_pool_reuses_released_buffers():
     before = C.pool_stats()
     bufs = [C.Buffer((1 << 20,)) for _ in range(4)]

@@ -109,6 +109,7 @@ _SIGNATURES = {
     "vc_hip_reduce_axis_noalloc": ([_vp, _vp, _sz, _sz, _sz, _i], _i),
     "vc_hip_scatter_axis": ([_vp, _vp, _vp, _sz, _sz, _sz], _i),
     "vc_hip_xent_forward": ([_vp, _vp, _sz, _sz, _vp, _vp], _i),
+    "vc_hip_xent_forward_published": ([_vp, _vp, _sz, _sz, _vp, _vp, ctypes.POINTER(_vp)], _i),
     "vc_hip_xent_backward": ([_vp, _vp, _vp, _vp, _sz, _sz, _vp], _i),
     "vc_hip_xent_backward_value": ([_vp, _vp, _vp, _f, _sz, _sz, _vp], _i),
     "vc_hip_xent_backward_colsum": ([_vp, _vp, _vp, _vp, _f, _sz, _sz, _vp, _vp], _i),

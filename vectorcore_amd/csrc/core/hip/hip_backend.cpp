@@ -165,6 +165,13 @@ public:
         if (elements_ != 1) return;
         vc_hip_mirror* m = nullptr;
         check(vc_hip_mirror_scalar(ptr(), &m), "HIP launch failed");
+        adopt_mirror(m);
+    }
+
+    // Takes a mirror already published from this one-element storage (its
+    // producer wrote the host slot, vc_hip_xent_forward_published).
+    void adopt_mirror(vc_hip_mirror* m) {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
         if (mirror_) (void)vc_hip_mirror_release(mirror_);
         mirror_ = m;
     }
@@ -1116,10 +1123,14 @@ std::pair<std::shared_ptr<Storage>, std::shared_ptr<Storage>> HipBackend::cross_
     require(*this);
     auto loss = fresh(1);
     auto stats = fresh(2 * rows);
-    check(vc_hip_xent_forward(dptr(logits, logits_offset), reinterpret_cast<const std::int32_t*>(as_hip(targets).ptr()),
-                              rows, classes, stats->ptr(), loss->ptr()),
+    // The loss is published as it is computed: loss.item() then waits for the
+    // forward only, not the backward and update after it.
+    vc_hip_mirror* published = nullptr;
+    check(vc_hip_xent_forward_published(dptr(logits, logits_offset),
+                                        reinterpret_cast<const std::int32_t*>(as_hip(targets).ptr()), rows, classes,
+                                        stats->ptr(), loss->ptr(), &published),
           "HIP cross-entropy failed");
-    loss->publish();  // loss.item() then waits for the forward only, not the backward and update after it
+    loss->adopt_mirror(published);
     return {loss, stats};
 }
 

@@ -282,6 +282,26 @@ Mirrors& mirrors() {
     return m;
 }
 
+}  // namespace
+
+vc_hip_mirror* take_mirror() { return mirrors().take(); }
+
+void give_mirror(vc_hip_mirror* m) noexcept {
+    try {
+        mirrors().give(m);
+    } catch (...) {  // a slot that cannot be listed again stays unused
+    }
+}
+
+void launch_mirror(vc_hip_mirror* m, const float* device_value) {
+    hipExtLaunchKernelGGL(mirror_kernel, dim3(1), dim3(64), 0, device().stream, nullptr, m->done, 0u, device_value,
+                          m->host);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) fail(VC_HIP_ERR_RUNTIME, std::string("launch of mirror_kernel failed: ") + hipGetErrorString(e));
+}
+
+namespace {
+
 // ---- profiler -----------------------------------------------------------------
 
 struct ProfRecord {
@@ -556,12 +576,12 @@ int vc_hip_mirror_scalar(const float* device_value, vc_hip_mirror** out) {
     return guard([&] {
         Device& d = require_device();
         if (!device_value || !out) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_mirror_scalar: null pointer");
-        vc_hip_mirror* m = mirrors().take();
-        hipExtLaunchKernelGGL(mirror_kernel, dim3(1), dim3(64), 0, d.stream, nullptr, m->done, 0u, device_value, m->host);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) {
-            mirrors().give(m);
-            fail(VC_HIP_ERR_RUNTIME, std::string("launch of mirror_kernel failed: ") + hipGetErrorString(e));
+        vc_hip_mirror* m = take_mirror();
+        try {
+            launch_mirror(m, device_value);
+        } catch (...) {
+            give_mirror(m);
+            throw;
         }
         *out = m;
     });

@@ -83,6 +83,14 @@ void after_launch(const char* label);
 // the object dies; stream order keeps the enqueued passes safe.
 void* pool_alloc(size_t bytes);
 void pool_release(void* p) noexcept;
+
+// Scalar mirrors (runtime.hip): a pinned host slot and its completion event,
+// taken from and given back to the library's free list; launch_mirror copies
+// a device value into the slot in stream order, the copy's dispatch carrying
+// the event.
+vc_hip_mirror* take_mirror();
+void give_mirror(vc_hip_mirror* m) noexcept;
+void launch_mirror(vc_hip_mirror* m, const float* device_value);
 class Scratch {
 public:
     explicit Scratch(size_t bytes) : p_(pool_alloc(bytes)) {}

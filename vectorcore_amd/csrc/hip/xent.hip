@@ -439,8 +439,10 @@ struct NegateDivide {
 // wave_terms. Block b adds them in wave order into its partial; the block
 // that finishes last adds all partials in block order (red::count_in,
 // red::finish_partials) and writes the loss.
+// With host_loss (pinned host memory), the loss is also written there, for a
+// reader that waits for this kernel's completion only.
 __device__ inline void finish_loss(double* wave_terms, double* __restrict__ part, int64_t rows,
-                                   float* __restrict__ loss) {
+                                   float* __restrict__ loss, float* __restrict__ host_loss) {
     __syncthreads();
     double sum = 0.0;
     if (threadIdx.x == 0) {
@@ -449,7 +451,11 @@ __device__ inline void finish_loss(double* wave_terms, double* __restrict__ part
     }
     if (!red::count_in(sum, part)) return;
     const double total = red::finish_partials(part, wave_terms);
-    if (threadIdx.x == 0) loss[0] = NegateDivide{float(rows)}(float(total));
+    if (threadIdx.x == 0) {
+        const float value = NegateDivide{float(rows)}(float(total));
+        loss[0] = value;
+        if (host_loss) host_loss[0] = value;
+    }
 }
 
 template <int NV, bool Vec>
@@ -458,7 +464,8 @@ template <int NV, bool Vec>
 __global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float* __restrict__ x,
                                                                   const int* __restrict__ targets, int64_t rows,
                                                                   int64_t len, float* __restrict__ stats,
-                                                                  double* __restrict__ part, float* __restrict__ loss) {
+                                                                  double* __restrict__ part, float* __restrict__ loss,
+                                                                  float* __restrict__ host_loss) {
     __shared__ double wave_terms[kRowsPerBlock];
     const int lane = threadIdx.x % kWave;
     const int64_t first = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
@@ -487,7 +494,7 @@ __global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float
         }
     }
     if (lane == 0) wave_terms[threadIdx.x / kWave] = total;
-    finish_loss(wave_terms, part, rows, loss);
+    finish_loss(wave_terms, part, rows, loss, host_loss);
 }
 
 // Rows of at most 1024 classes, two per wavefront (finish_half_row): wave w
@@ -501,7 +508,8 @@ template <int NV, bool Vec>
 __global__ __launch_bounds__(kBlock, 5) void xent_half_rows_kernel(const float* __restrict__ x,
                                                                    const int* __restrict__ targets, int64_t rows,
                                                                    int64_t len, float* __restrict__ stats,
-                                                                   double* __restrict__ part, float* __restrict__ loss) {
+                                                                   double* __restrict__ part, float* __restrict__ loss,
+                                                                   float* __restrict__ host_loss) {
     __shared__ double wave_terms[kRowsPerBlock];
     const int lane = threadIdx.x % kWave, h = lane >> 5;
     const int64_t wave_id = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
@@ -520,7 +528,7 @@ __global__ __launch_bounds__(kBlock, 5) void xent_half_rows_kernel(const float* 
     const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(tb >> 32)), 32));
     const double upper = __builtin_bit_cast(double, uint64_t(lo) | (uint64_t(hi) << 32));
     if (lane == 0) wave_terms[threadIdx.x / kWave] = total + upper;
-    finish_loss(wave_terms, part, rows, loss);
+    finish_loss(wave_terms, part, rows, loss, host_loss);
 }
 
 // One wavefront per row, streaming the row twice (rows too long for
@@ -711,6 +719,84 @@ void xent_backward(const float* logits, const int32_t* targets, const float* row
     p.done();
 }
 
+// The forward. With `publish`, the loss is also copied into that mirror's
+// host slot: by the finishing block of a register-held row kernel, whose
+// dispatch then carries the mirror's completion event, or, when the profiler
+// holds the dispatch's events or the rows are streamed, by a copy launched
+// after the forward.
+void xent_forward(const float* logits, const int32_t* targets, size_t rows, size_t classes, float* row_stats,
+                  float* loss, vc_hip_mirror* publish) {
+    Device& d = require_device();
+    if (rows == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "cross_entropy of an empty batch is undefined");
+    if (classes == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "cross_entropy needs at least one class");
+    if (classes > size_t(std::numeric_limits<int>::max())) fail(VC_HIP_ERR_OVERFLOW, "too many classes");
+    const int64_t R = int64_t(rows), C = int64_t(classes);
+    Scratch terms(rows * sizeof(float));
+    const bool vec = C % 4 == 0 && aligned16(logits);
+    const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
+    Profiled p("xent_forward", 0.0, 4.0 * double(R * C) + 4.0 * double(R) + 8.0 * double(R));
+    // Rows are held in registers: up to 1024 classes two rows per wavefront,
+    // up to 4096 one row per wavefront (NV float4 per lane); at most 8
+    // workgroups per CU walk the rows (3 to 12 per CU measured within 3%).
+    // Longer rows are streamed.
+    const int64_t nv = (C + kWave * 4 - 1) / (kWave * 4);
+    const unsigned cached_grid = unsigned(std::min<int64_t>(
+        {(R + kRowsPerBlock - 1) / kRowsPerBlock, int64_t(d.cu_count) * kXentBlocksPerCu,
+         int64_t(red::kMaxFinishBlocks)}));
+    Scratch part(size_t(std::max<int64_t>(cached_grid, (R + red::sum_chunk(R) - 1) / red::sum_chunk(R))) *
+                 sizeof(double));
+    // Register-held rows (nv <= 16) write the loss's host copy from their
+    // finishing block, the dispatch signalling the mirror, unless the
+    // profiler holds the dispatch's events.
+    float* host_loss = nullptr;
+    hipEvent_t published = nullptr;
+    if (publish && nv <= 16 && !p.stop_event()) {
+        host_loss = publish->host;
+        published = publish->done;
+    }
+    auto row_launch = [&](auto kernel, unsigned blocks) {
+        if (published)
+            hipExtLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlock), 0, d.stream, nullptr, published, 0u, logits,
+                                  targets, R, C, row_stats, part.as<double>(), loss, host_loss);
+        else
+            launch(kernel, dim3(blocks), dim3(kBlock), 0, d.stream, logits, targets, R, C, row_stats,
+                   part.as<double>(), loss, host_loss);
+    };
+    const int64_t nh = (C + 127) / 128;  // float4s per lane with a half-wave per row
+    if (nh <= 8) {
+        // Rows of at most 1024 classes: two per wavefront.
+        const unsigned half_grid = unsigned(std::min<int64_t>(
+            {(R + 2 * kRowsPerBlock - 1) / (2 * kRowsPerBlock), int64_t(d.cu_count) * kXentBlocksPerCu,
+             int64_t(red::kMaxFinishBlocks)}));
+#define VC_XENT_HALF(NV) row_launch(vec ? xent_half_rows_kernel<NV, true> : xent_half_rows_kernel<NV, false>, half_grid)
+        if (nh <= 1) VC_XENT_HALF(1);
+        else if (nh <= 2) VC_XENT_HALF(2);
+        else if (nh <= 4) VC_XENT_HALF(4);
+        else VC_XENT_HALF(8);
+#undef VC_XENT_HALF
+    } else if (nv > 16) {
+        // Row terms, then the shared deterministic full sum (one launch).
+        launch((vec ? xent_rows_kernel<true> : xent_rows_kernel<false>), dim3(grid), dim3(kBlock), 0, d.stream,
+               logits, targets, R, C, row_stats, terms.as<float>());
+        after_launch("xent_forward");
+        const int64_t chunk = red::sum_chunk(R);
+        const int64_t blocks = (R + chunk - 1) / chunk;
+        launch(red::sum_finish_kernel<true, NegateDivide>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream,
+               terms.as<float>(), part.as<double>(), loss, R, chunk, NegateDivide{float(R)});
+    } else {
+        // Register-held rows; the row kernel sums the terms per block and
+        // its last block finishes the loss.
+#define VC_XENT_ROWS(NV) \
+    row_launch(vec ? xent_rows_cached_kernel<NV, true> : xent_rows_cached_kernel<NV, false>, cached_grid)
+        if (nv <= 8) VC_XENT_ROWS(8);  // rows of more than 1024 classes: nv >= 5
+        else VC_XENT_ROWS(16);
+#undef VC_XENT_ROWS
+    }
+    after_launch("xent_forward");
+    if (publish && !host_loss) launch_mirror(publish, loss);
+    p.done();
+}
+
 }  // namespace
 }  // namespace vchip
 
@@ -720,61 +806,22 @@ extern "C" {
 
 int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows, size_t classes, float* row_stats,
                         float* loss) {
+    return guard([&] { xent_forward(logits, targets, rows, classes, row_stats, loss, nullptr); });
+}
+
+int vc_hip_xent_forward_published(const float* logits, const int32_t* targets, size_t rows, size_t classes,
+                                  float* row_stats, float* loss, vc_hip_mirror** mirror) {
     return guard([&] {
-        Device& d = require_device();
-        if (rows == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "cross_entropy of an empty batch is undefined");
-        if (classes == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "cross_entropy needs at least one class");
-        if (classes > size_t(std::numeric_limits<int>::max())) fail(VC_HIP_ERR_OVERFLOW, "too many classes");
-        const int64_t R = int64_t(rows), C = int64_t(classes);
-        Scratch terms(rows * sizeof(float));
-        const bool vec = C % 4 == 0 && aligned16(logits);
-        const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
-        Profiled p("xent_forward", 0.0, 4.0 * double(R * C) + 4.0 * double(R) + 8.0 * double(R));
-        // Rows are held in registers: up to 1024 classes two rows per wavefront,
-        // up to 4096 one row per wavefront (NV float4 per lane); at most 8
-        // workgroups per CU walk the rows (3 to 12 per CU measured within 3%).
-        // Longer rows are streamed.
-        const int64_t nv = (C + kWave * 4 - 1) / (kWave * 4);
-        const unsigned cached_grid = unsigned(std::min<int64_t>(
-            {(R + kRowsPerBlock - 1) / kRowsPerBlock, int64_t(d.cu_count) * kXentBlocksPerCu,
-             int64_t(red::kMaxFinishBlocks)}));
-        Scratch part(size_t(std::max<int64_t>(cached_grid, (R + red::sum_chunk(R) - 1) / red::sum_chunk(R))) *
-                     sizeof(double));
-        const int64_t nh = (C + 127) / 128;  // float4s per lane with a half-wave per row
-        if (nh <= 8) {
-            // Rows of at most 1024 classes: two per wavefront.
-            const unsigned half_grid = unsigned(std::min<int64_t>(
-                {(R + 2 * kRowsPerBlock - 1) / (2 * kRowsPerBlock), int64_t(d.cu_count) * kXentBlocksPerCu,
-                 int64_t(red::kMaxFinishBlocks)}));
-#define VC_XENT_HALF(NV)                                                                                        \
-    launch(vec ? xent_half_rows_kernel<NV, true> : xent_half_rows_kernel<NV, false>, dim3(half_grid), dim3(kBlock), \
-           0, d.stream, logits, targets, R, C, row_stats, part.as<double>(), loss)
-            if (nh <= 1) VC_XENT_HALF(1);
-            else if (nh <= 2) VC_XENT_HALF(2);
-            else if (nh <= 4) VC_XENT_HALF(4);
-            else VC_XENT_HALF(8);
-#undef VC_XENT_HALF
-        } else if (nv > 16) {
-            // Row terms, then the shared deterministic full sum (one launch).
-            launch((vec ? xent_rows_kernel<true> : xent_rows_kernel<false>), dim3(grid), dim3(kBlock), 0, d.stream,
-                   logits, targets, R, C, row_stats, terms.as<float>());
-            after_launch("xent_forward");
-            const int64_t chunk = red::sum_chunk(R);
-            const int64_t blocks = (R + chunk - 1) / chunk;
-            launch(red::sum_finish_kernel<true, NegateDivide>, dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream,
-                   terms.as<float>(), part.as<double>(), loss, R, chunk, NegateDivide{float(R)});
-        } else {
-            // Register-held rows; the row kernel sums the terms per block and
-            // its last block finishes the loss.
-#define VC_XENT_ROWS(NV)                                                                                          \
-    launch(vec ? xent_rows_cached_kernel<NV, true> : xent_rows_cached_kernel<NV, false>, dim3(cached_grid),     \
-           dim3(kBlock), 0, d.stream, logits, targets, R, C, row_stats, part.as<double>(), loss)
-            if (nv <= 8) VC_XENT_ROWS(8);  // rows of more than 1024 classes: nv >= 5
-            else VC_XENT_ROWS(16);
-#undef VC_XENT_ROWS
+        if (!mirror) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_xent_forward_published: null mirror");
+        require_device();
+        vc_hip_mirror* m = take_mirror();
+        try {
+            xent_forward(logits, targets, rows, classes, row_stats, loss, m);
+        } catch (...) {
+            give_mirror(m);
+            throw;
         }
-        after_launch("xent_forward");
-        p.done();
+        *mirror = m;
     });
 }
 

@@ -28,7 +28,8 @@ def reduce(fn, dx, outer, length, inner, op):
 # (outer, length, inner, op) pairs: a larger call, then a smaller one of the
 # same kind right after it on the same static array.
 PAIRS = [
-    ((1, 8192, 4096, C.SUM), (1, 3000, 1000, C.SUM)),    # bias gradients: one launch (1 MiB), then a combine (184 KB)
+    ((1, 8192, 4096, C.SUM), (1, 3000, 1000, C.SUM)),    # bias gradients: one launch of ~2048 blocks (1 MiB), one of ~128
+    ((1, 8192, 1000, C.SUM), (1, 3000, 300, C.SUM)),     # narrow one launch, then partials and a combine launch
     ((1, 8192, 4096, C.SUM), (1, 4000, 2048, C.SUM)),    # one-launch column sums twice: the chunk counters reset
     ((3, 700, 999, C.SUM), (2, 300, 37, C.SUM)),         # scalar loads, several outer blocks
     ((1, 5000, 300, C.ARGMAX), (1, 900, 70, C.ARGMAX)),  # a long axis split into segments

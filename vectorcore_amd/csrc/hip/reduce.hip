@@ -483,14 +483,17 @@ ColumnPlan column_plan(const float* in, int64_t outer, int64_t len, int64_t inne
     return c;
 }
 
-// The one-launch column sum (outer 1): about 2048 blocks, segments of at
-// least 16 rows, at most 32 segments (the blocks of a chunk count in on one
-// counter, and atomics on one address are served one at a time: 128 segments
-// per chunk measured 2.5x slower than 32); a function of the shape only.
-// Used from 32 chunks (2048 columns) up: with fewer chunks the blocks are too
-// few to stream the matrix at full rate and the two-launch path is faster
-// (8192 x 1000: 13.6 us against 12.4 us; 8192 x 4096: 23.9 us against 26.1 us).
-constexpr int64_t kFinishMinChunks = 32;
+// The one-launch column sum (outer 1): about 2048 blocks from 32 chunks
+// (2048 columns) up, about 128 from 8 to 31 chunks; segments of at least 16
+// rows, at most 32 segments (the blocks of a chunk count in on one counter,
+// and atomics on one address are served one at a time: 128 segments per chunk
+// measured 2.5x slower than 32); a function of the shape only. Narrow sums
+// take few, long segments: with 512 blocks their counters queued and
+// 8192 x 1000 took 13.9 us, against 12.1-12.4 us for 128 blocks and for the
+// two-launch path, which 4096 x 1000 takes in 8.9 us against 7.3 us here.
+// Below 8 chunks the two-launch path runs. (8192 x 4096 takes 23.9 us in one
+// launch against 26.1 us in two.)
+constexpr int64_t kFinishMinChunks = 8, kFinishWideChunks = 32;
 struct FinishPlan {
     bool vec;
     int64_t chunks, segs, seg_len;
@@ -501,7 +504,8 @@ FinishPlan finish_plan(const float* in, int64_t len, int64_t inner) {
     f.vec = inner % 4 == 0 && aligned16(in);
     const int64_t width = f.vec ? 4 * kColLanes : kColLanes;
     f.chunks = (inner + width - 1) / width;
-    int64_t segs = std::max<int64_t>(1, (2048 + f.chunks - 1) / f.chunks);
+    const int64_t blocks = f.chunks >= kFinishWideChunks ? 2048 : 128;
+    int64_t segs = std::max<int64_t>(1, (blocks + f.chunks - 1) / f.chunks);
     segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / 16), int64_t(32)});
     f.seg_len = (len + segs - 1) / segs;
     f.segs = (len + f.seg_len - 1) / f.seg_len;

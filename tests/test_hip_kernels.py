@@ -359,7 +359,7 @@ def reduce_axis_dev(x, axis, op):
 
 @pytest.mark.parametrize("shape", [(64, 500, 33), (5, 300, 7), (4096, 4096), (8192, 1000), (3, 4, 5), (1, 3_000_001),
                                    (8, 1024 * 1024), (3001, 2051), (70, 8192), (2049, 2048), (1000, 700), (3001, 301),
-                                   (3000, 300), (2000, 512), (2000, 448), (1500, 2044)])
+                                   (3000, 300), (2000, 512), (2000, 448), (1500, 2044), (2000, 2047), (700, 250)])
 def test_reduce_axis_against_oracle(shape):
     # Column sums of one matrix with at least 8 column chunks (64 columns
     # each with 16-byte loads, 16 with scalar loads) take the one-launch
@@ -370,7 +370,10 @@ def test_reduce_axis_against_oracle(shape):
     # with a short last chunk and (3001, 301) with scalar loads. (3000, 300)
     # has 5 chunks: partials, then a combine launch. At the boundaries:
     # (2000, 512) has 8 chunks (one launch), (2000, 448) 7 (two launches),
-    # (1500, 2044) 32 with a short last one (about 2048 blocks).
+    # (1500, 2044) 32 with a short last one (about 2048 blocks). Rows that
+    # are not whole 128-byte lines with a chunk count divisible by 8 give
+    # each XCD a contiguous run of chunks: (8192, 1000), (1500, 2044), and
+    # with scalar loads (2000, 2047) and (700, 250).
     rng = np.random.default_rng(len(shape) + shape[-1])
     x = rng.standard_normal(shape).astype(np.float32)
     for axis in range(len(shape)):

@@ -262,7 +262,19 @@ __global__ __launch_bounds__(kBlock) void colsum_finish_kernel(const float* __re
     __shared__ int last_block;
     const int c = threadIdx.x % kColLanes, rl = threadIdx.x / kColLanes;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const int64_t chunk = blockIdx.x, s = blockIdx.y, segs = gridDim.y;
+    // Workgroups go to the 8 XCDs round robin by linear id. When a row is not
+    // whole 128-byte lines, neighbouring chunks share lines at their edges:
+    // each XCD then takes a contiguous run of chunks, so that most shared
+    // lines are fetched into one XCD's L2 (8192 x 1000: 39 MB fetched instead
+    // of 46 MB, 11.3 us instead of 12.3 us).
+    int64_t chunk = blockIdx.x, s = blockIdx.y;
+    const int64_t segs = gridDim.y, nchunks = gridDim.x;
+    if (nchunks % 8 == 0 && (inner * int64_t(sizeof(float))) % 128 != 0) {
+        const int64_t linear = int64_t(blockIdx.x) + int64_t(blockIdx.y) * nchunks;
+        const int64_t per = nchunks / 8, j = linear / 8;
+        chunk = (linear % 8) * per + j % per;
+        s = j / per;
+    }
     const int64_t col = (chunk * kColLanes + c) * W;
     const int64_t a0 = s * seg_len, a1 = std::min(len, a0 + seg_len);
     double acc[W];

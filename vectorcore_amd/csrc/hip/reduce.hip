@@ -266,7 +266,8 @@ __global__ __launch_bounds__(kBlock) void colsum_finish_kernel(const float* __re
     // whole 128-byte lines, neighbouring chunks share lines at their edges:
     // each XCD then takes a contiguous run of chunks, so that most shared
     // lines are fetched into one XCD's L2 (8192 x 1000: 39 MB fetched instead
-    // of 46 MB, 11.3 us instead of 12.3 us).
+    // of 46 MB, 11.3 us instead of 12.3 us). Rows of whole lines keep the
+    // plain order: remapped, 8192 x 4096 took 26.2 us instead of 24.2 us.
     int64_t chunk = blockIdx.x, s = blockIdx.y;
     const int64_t segs = gridDim.y, nchunks = gridDim.x;
     if (nchunks % 8 == 0 && (inner * int64_t(sizeof(float))) % 128 != 0) {

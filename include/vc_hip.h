@@ -108,6 +108,12 @@ int vc_hip_mirror_release(vc_hip_mirror* mirror);
 /* MetalBackend::synchronize (metal_backend.hpp:55): waits and reports any
  * asynchronous device error. */
 int vc_hip_synchronize(void);
+/* Non-waiting query of the library stream: *idle = 1 when everything enqueued
+ * so far has completed (or no device was initialised), else 0. Fails with an
+ * error the stream has already recorded. No counterpart in the reference; it
+ * lets a caller check whether a read returned before or after the queue
+ * drained (see VECTORCORE_HIP_STRICT_ITEM in the C++ wrapper). */
+int vc_hip_stream_idle(int* idle);
 
 typedef struct vc_hip_pool_stats {
     uint64_t device_allocations; /* hipMalloc calls made by the pool */
@@ -118,6 +124,26 @@ typedef struct vc_hip_pool_stats {
 int vc_hip_pool_stats_get(vc_hip_pool_stats* out);
 /* Returns every parked buffer to the device (waits for queued work). */
 int vc_hip_pool_trim(void);
+
+/* ---- pending column sums ---------------------------------------------------- */
+/* The column sums of a matrix, left by the kernel that wrote it as partial
+ * rows of double sums (every matrix row counted in exactly one) in a pool
+ * buffer the handle owns: the *_colsum_pending entry points below return one.
+ * Finishing adds the partial rows in one fixed order and rounds once to
+ * float; vc_hip_colsum_finish and vc_hip_axpy_batch_colsum do it with the same
+ * arithmetic, so both give the same bits, and a handle may be finished any
+ * number of times until released. No counterpart in the reference: a bias
+ * gradient there is a separate sum_to_shape pass over its operand's gradient
+ * (src/autograd.cpp:50-72, src/cpu/cpu_backend.cpp:420-441); here it costs no
+ * launch of its own when the optimizer step is its only reader. */
+typedef struct vc_hip_colsum vc_hip_colsum;
+/* column_sum[j] (n floats) = the finished sums, enqueued on the stream. */
+int vc_hip_colsum_finish(const vc_hip_colsum* sums, float* column_sum);
+/* *columns = n, the number of column sums. */
+int vc_hip_colsum_size(const vc_hip_colsum* sums, size_t* columns);
+/* Returns the partial rows to the pool in stream order (work already
+ * enqueued that reads them is unaffected). NULL is accepted. */
+int vc_hip_colsum_release(vc_hip_colsum* sums);
 
 /* ---- elementwise ----------------------------------------------------------- */
 int vc_hip_fill(float* out, size_t count, float value);
@@ -143,6 +169,17 @@ int vc_hip_axpy(float* target, const float* source, size_t count, float alpha);
  * (metal_backend.hpp:53-54) to each parameter in turn. */
 int vc_hip_axpy_batch(float* const* outputs, const float* const* targets, const float* const* sources,
                       const size_t* counts, size_t tensors, float alpha);
+/* vc_hip_axpy_batch where entry k's source may be pending column sums:
+ * with sums != NULL and sums[k] != NULL, outputs[k][j] = targets[k][j] +
+ * alpha * (the finished sum j of sums[k]) for j < counts[k] (which must equal
+ * its column count; sources[k] is not read), the same bits as
+ * vc_hip_colsum_finish into a buffer followed by vc_hip_axpy_batch. The sums
+ * are finished inside the same launch (blocks that run beside the other
+ * tensors' updates) and the handles stay valid. No counterpart in the
+ * reference: nn::sgd_step (src/nn.cpp:55-76) applying a bias gradient that
+ * was never materialised. */
+int vc_hip_axpy_batch_colsum(float* const* outputs, const float* const* targets, const float* const* sources,
+                             const vc_hip_colsum* const* sums, const size_t* counts, size_t tensors, float alpha);
 
 /* Fused activation gradients (one pass each; same-shape contiguous operands).
  * relu:    out = grad * (input > 0 ? 1 : 0)         (src/ops.cpp:398-401)
@@ -239,6 +276,15 @@ int vc_hip_matmul_relu_mask(const float* a, const float* b, float* c, size_t m, 
  * src/cpu/cpu_backend.cpp:420-441). k must be > 0 unless m is 0. */
 int vc_hip_matmul_relu_mask_colsum(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
                                    int trans_a, int trans_b, const float* mask, float* column_sum);
+/* vc_hip_matmul_relu_mask_colsum whose column sums may stay pending: when the
+ * product's kernel keeps per-tile partial rows (any product not split along
+ * K), *pending receives a handle to them and column_sum is not written;
+ * otherwise *pending is NULL and column_sum is written as
+ * vc_hip_matmul_relu_mask_colsum writes it. Finishing the handle gives the
+ * bits vc_hip_matmul_relu_mask_colsum writes. Serves the same rules. */
+int vc_hip_matmul_relu_mask_colsum_pending(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                                           int trans_a, int trans_b, const float* mask, float* column_sum,
+                                           vc_hip_colsum** pending);
 /* A forward layer in one kernel: c = a @ b (+ bias[column]) (then ReLU),
  * a [m][k], b [k][n], bias [n] or null, all contiguous; relu nonzero applies
  * x > 0 ? x : 0 after the bias. The same bits as vc_hip_matmul, then the
@@ -301,6 +347,15 @@ int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows
  * (metal_backend.mm:198-211). */
 int vc_hip_xent_forward_published(const float* logits, const int32_t* targets, size_t rows, size_t classes,
                                   float* row_stats, float* loss, vc_hip_mirror** mirror);
+/* vc_hip_xent_forward (mirror NULL) or vc_hip_xent_forward_published, whose
+ * kernel also writes row_argmax[i] = the index of row i's first strict
+ * maximum as a float (a NaN element 0 wins): the same values as
+ * vc_hip_reduce_axis(logits, row_argmax, rows, classes, 1, VC_REDUCE_ARGMAX),
+ * from the rows the forward already reads. No counterpart in the reference,
+ * which reads the logits again for argmax (src/ops.cpp:354-358,
+ * src/cpu/cpu_backend.cpp:443-457) after the loss (src/nn.cpp:31-53). */
+int vc_hip_xent_forward_argmax(const float* logits, const int32_t* targets, size_t rows, size_t classes,
+                               float* row_stats, float* loss, float* row_argmax, vc_hip_mirror** mirror);
 /* grad_logits = (softmax(logits) - onehot(targets)) * grad_loss[0] / rows,
  * evaluated as the reference's composed backward does. grad_loss is a device
  * scalar (the upstream gradient of the loss). */
@@ -325,6 +380,13 @@ int vc_hip_xent_backward_value(const float* logits, const int32_t* targets, cons
 int vc_hip_xent_backward_colsum(const float* logits, const int32_t* targets, const float* row_stats,
                                 const float* grad_loss, float grad_loss_value, size_t rows, size_t classes,
                                 float* grad_logits, float* column_sum);
+/* vc_hip_xent_backward_colsum whose column sums may stay pending (rows of at
+ * most 2048 classes, whose kernel keeps one partial row per 16 rows):
+ * *pending then receives the handle and column_sum is not written;
+ * otherwise *pending is NULL and column_sum is written. */
+int vc_hip_xent_backward_colsum_pending(const float* logits, const int32_t* targets, const float* row_stats,
+                                        const float* grad_loss, float grad_loss_value, size_t rows, size_t classes,
+                                        float* grad_logits, float* column_sum, vc_hip_colsum** pending);
 
 /* ---- measurement ------------------------------------------------------------- */
 /* When enabled, the kernels of each labelled entry-point call carry HIP

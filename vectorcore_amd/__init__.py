@@ -17,6 +17,7 @@ from ._vectorcore import (  # noqa: F401
     hip_fuse_elementwise,
     hip_gemm_kernel,
     hip_set_gemm_kernel,
+    hip_strict_item,
     hip_pool_stats,
     hip_profile,
     hip_profile_read,

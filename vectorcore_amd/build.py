@@ -16,6 +16,7 @@ recompiles; objects go to vectorcore_amd/_build/, libraries next to this file.
 from __future__ import annotations
 
 import os
+import re
 import subprocess
 import sys
 import sysconfig
@@ -62,16 +63,38 @@ def _parallel(fn, items):
         return list(pool.map(fn, items))
 
 
+def _scratch_kernels(log: str) -> list[tuple[str, int]]:
+    """Kernels that the compiler's resource report (-Rpass-analysis=
+    kernel-resource-usage) gives a nonzero ScratchSize: register spills to
+    memory, which every kernel here is written to avoid."""
+    spills, name = [], None
+    for line in log.splitlines():
+        m = re.search(r"remark:\s*Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"remark:\s*ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and name and int(m.group(1)) > 0:
+            spills.append((name, int(m.group(1))))
+    return spills
+
+
 def build_hip(verbose: bool = False) -> Path:
-    """Compile the HIP kernels and the C ABI into libvc_hip.so."""
+    """Compile the HIP kernels and the C ABI into libvc_hip.so. Fails when any
+    kernel spills registers to scratch memory."""
     OBJ.mkdir(exist_ok=True)
 
     def compile_one(job) -> Path:
         src, defines, tag = job
         obj = OBJ / (Path(src).stem + tag + ".hip.o")
-        log = _run([HIPCC, *HIP_FLAGS, *defines, "-c", str(CSRC / "hip" / src), "-o", str(obj)])
-        if verbose and log:
-            print(log, file=sys.stderr)
+        log = _run([HIPCC, *HIP_FLAGS, *defines, "-Rpass-analysis=kernel-resource-usage", "-c",
+                    str(CSRC / "hip" / src), "-o", str(obj)])
+        spills = _scratch_kernels(log)
+        if spills:
+            raise RuntimeError(f"{src} {' '.join(defines)}: kernels spill to scratch memory "
+                               f"(bytes per lane): {spills}")
+        if verbose:
+            print("\n".join(l for l in log.splitlines() if "remark:" not in l), file=sys.stderr)
         return obj
 
     jobs = [(src, [], "") for src in HIP_SOURCES]

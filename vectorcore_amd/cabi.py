@@ -84,14 +84,20 @@ _SIGNATURES = {
     "vc_hip_mirror_release": ([_vp], _i),
     "vc_hip_copy": ([_vp, _vp, _sz], _i),
     "vc_hip_synchronize": ([], _i),
+    "vc_hip_stream_idle": ([ctypes.POINTER(_i)], _i),
     "vc_hip_pool_stats_get": ([_vp], _i),
     "vc_hip_pool_trim": ([], _i),
+    "vc_hip_colsum_finish": ([_vp, _vp], _i),
+    "vc_hip_colsum_size": ([_vp, _szp], _i),
+    "vc_hip_colsum_release": ([_vp], _i),
     "vc_hip_fill": ([_vp, _sz, _f], _i),
     "vc_hip_binary": ([_vp, _szp, _szp, _sz, _vp, _szp, _szp, _sz, _vp, _szp, _sz, _i], _i),
     "vc_hip_binary_scalar": ([_vp, _sz, _f, _i, _vp, _i], _i),
     "vc_hip_unary": ([_vp, _vp, _sz, _i], _i),
     "vc_hip_axpy": ([_vp, _vp, _sz, _f], _i),
     "vc_hip_axpy_batch": ([ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp), _szp, _sz, _f], _i),
+    "vc_hip_axpy_batch_colsum": ([ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                                  ctypes.POINTER(_vp), _szp, _sz, _f], _i),
     "vc_hip_relu_backward": ([_vp, _vp, _vp, _sz], _i),
     "vc_hip_sigmoid_backward": ([_vp, _vp, _vp, _sz], _i),
     "vc_hip_exp_backward": ([_vp, _vp, _vp, _sz], _i),
@@ -101,6 +107,8 @@ _SIGNATURES = {
     "vc_hip_matmul": ([_vp, _vp, _vp, _sz, _sz, _sz, _szp, _szp, _sz, _i, _i], _i),
     "vc_hip_matmul_relu_mask": ([_vp, _vp, _vp, _sz, _sz, _sz, _szp, _szp, _sz, _i, _i, _vp], _i),
     "vc_hip_matmul_relu_mask_colsum": ([_vp, _vp, _vp, _sz, _sz, _sz, _i, _i, _vp, _vp], _i),
+    "vc_hip_matmul_relu_mask_colsum_pending": ([_vp, _vp, _vp, _sz, _sz, _sz, _i, _i, _vp, _vp,
+                                                ctypes.POINTER(_vp)], _i),
     "vc_hip_matmul_bias_relu": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp, _i], _i),
     "vc_hip_matmul_reduce": ([_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _i], _i),
     "vc_hip_transpose_last2": ([_vp, _vp, _sz, _sz, _sz], _i),
@@ -110,9 +118,11 @@ _SIGNATURES = {
     "vc_hip_scatter_axis": ([_vp, _vp, _vp, _sz, _sz, _sz], _i),
     "vc_hip_xent_forward": ([_vp, _vp, _sz, _sz, _vp, _vp], _i),
     "vc_hip_xent_forward_published": ([_vp, _vp, _sz, _sz, _vp, _vp, ctypes.POINTER(_vp)], _i),
+    "vc_hip_xent_forward_argmax": ([_vp, _vp, _sz, _sz, _vp, _vp, _vp, ctypes.POINTER(_vp)], _i),
     "vc_hip_xent_backward": ([_vp, _vp, _vp, _vp, _sz, _sz, _vp], _i),
     "vc_hip_xent_backward_value": ([_vp, _vp, _vp, _f, _sz, _sz, _vp], _i),
     "vc_hip_xent_backward_colsum": ([_vp, _vp, _vp, _vp, _f, _sz, _sz, _vp, _vp], _i),
+    "vc_hip_xent_backward_colsum_pending": ([_vp, _vp, _vp, _vp, _f, _sz, _sz, _vp, _vp, ctypes.POINTER(_vp)], _i),
     "vc_hip_profile_enable": ([_i], _i),
     "vc_hip_profile_labels": ([ctypes.c_char_p], _i),
     "vc_hip_profile_reset": ([], _i),
@@ -159,6 +169,13 @@ def available() -> bool:
 
 def synchronize() -> None:
     check(lib().vc_hip_synchronize())
+
+
+def stream_idle() -> bool:
+    """Whether the library stream has completed everything enqueued (no wait)."""
+    idle = ctypes.c_int(-1)
+    check(lib().vc_hip_stream_idle(ctypes.byref(idle)))
+    return bool(idle.value)
 
 
 def pool_stats() -> PoolStats:

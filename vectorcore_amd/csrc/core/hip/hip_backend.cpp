@@ -107,6 +107,7 @@ public:
 
     ~HipStorage() override {
         if (mirror_) (void)vc_hip_mirror_release(mirror_);
+        if (pending_sums_) (void)vc_hip_colsum_release(pending_sums_);
         if (ptr_) (void)vc_hip_release(ptr_);
     }
     HipStorage(const HipStorage&) = delete;
@@ -126,6 +127,11 @@ public:
         if (!ptr_) {
             check(vc_hip_alloc(bytes(), &ptr_), "HIP allocation failed");
             if (!shadow_.empty()) check(vc_hip_upload(ptr_, shadow_.data(), shadow_.size() * sizeof(float)), "HIP upload failed");
+        }
+        if (pending_sums_) {
+            check(vc_hip_colsum_finish(pending_sums_, static_cast<float*>(ptr_)), "HIP column sum failed");
+            (void)vc_hip_colsum_release(pending_sums_);
+            pending_sums_ = nullptr;
         }
         if (deferred_) {
             const DeferredProduct& d = *deferred_;
@@ -193,6 +199,39 @@ public:
         return std::move(column_sum_);
     }
 
+    // This storage's values are the column sums that `sums` leaves pending
+    // (the partial rows of the kernel that wrote the summed matrix); they are
+    // finished into the buffer on first read, and an optimizer step can take
+    // them unfinished (pending_sums).
+    void set_pending_sums(vc_hip_colsum* sums) {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        if (pending_sums_) (void)vc_hip_colsum_release(pending_sums_);
+        pending_sums_ = sums;
+    }
+    const vc_hip_colsum* pending_sums() const {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        return pending_sums_;
+    }
+
+    // Argmax along the last axis of this storage's [rows, cols] view at
+    // `offset`, computed by a kernel that read those rows (the cross-entropy
+    // forward). Kept until taken or until the storage is written in place.
+    void set_row_argmax(std::shared_ptr<HipStorage> indices, std::size_t offset, std::size_t rows,
+                        std::size_t cols) const {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        row_argmax_ = std::move(indices);
+        row_argmax_offset_ = offset;
+        row_argmax_rows_ = rows;
+        row_argmax_cols_ = cols;
+    }
+    // The argmax kept for exactly that view, once.
+    std::shared_ptr<HipStorage> take_row_argmax(std::size_t offset, std::size_t rows, std::size_t cols) const {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        if (!row_argmax_ || offset != row_argmax_offset_ || rows != row_argmax_rows_ || cols != row_argmax_cols_)
+            return nullptr;
+        return std::move(row_argmax_);
+    }
+
     // The deferred product this storage still has to compute, if any (a copy
     // for building a product with a longer epilogue).
     std::optional<DeferredProduct> pending() const {
@@ -238,6 +277,7 @@ public:
         (void)ptr();
         shadow_valid_ = false;
         column_sum_.reset();  // about to be stale
+        row_argmax_.reset();
         if (mirror_) {  // the published value is about to be stale
             (void)vc_hip_mirror_release(mirror_);
             mirror_ = nullptr;
@@ -288,8 +328,11 @@ private:
     std::size_t sum_rows_ = 0;
     std::vector<std::weak_ptr<HipStorage>> readers_;
     vc_hip_mirror* mirror_ = nullptr;  // published value of a one-element result
+    mutable vc_hip_colsum* pending_sums_ = nullptr;  // see set_pending_sums
     mutable std::shared_ptr<HipStorage> column_sum_;  // see set_column_sum
     std::size_t column_sum_rows_ = 0, column_sum_cols_ = 0;
+    mutable std::shared_ptr<HipStorage> row_argmax_;  // see set_row_argmax
+    mutable std::size_t row_argmax_offset_ = 0, row_argmax_rows_ = 0, row_argmax_cols_ = 0;
     bool shadow_valid_;
 };
 
@@ -645,9 +688,23 @@ std::shared_ptr<Storage> HipBackend::upload(const float* data, std::size_t eleme
     return out;
 }
 
+namespace {
+std::atomic<bool>& strict_item_flag() {
+    static std::atomic<bool> flag{[] {
+        const char* v = std::getenv("VECTORCORE_HIP_STRICT_ITEM");
+        return v && std::string(v) == "1";
+    }()};
+    return flag;
+}
+}  // namespace
+
+void HipBackend::set_strict_item(bool enable) { strict_item_flag() = enable; }
+bool HipBackend::strict_item() const { return strict_item_flag(); }
+
 void HipBackend::download(const Storage& source, std::size_t offset, float* destination, std::size_t elements) {
     if (offset + elements > source.size()) throw std::out_of_range("HIP download exceeds storage");
     const auto& h = as_hip(source);
+    if (strict_item()) synchronize();
     if (h.host_copy(offset, destination, elements)) return;
     check(vc_hip_download(destination, h.ptr() + offset, elements * sizeof(float)), "HIP command failed");
 }
@@ -766,9 +823,12 @@ std::shared_ptr<Storage> HipBackend::matmul_relu_mask(const Storage& a, std::siz
     }
     if (column_sum && batch == 1 && a_offsets[0] == 0 && b_offsets[0] == 0) {
         auto sums = fresh(n);
-        check(vc_hip_matmul_relu_mask_colsum(dptr(a, a_offset), dptr(b, b_offset), out->ptr(), m, k, n, trans_a ? 1 : 0,
-                                             trans_b ? 1 : 0, dptr(mask, mask_offset), sums->ptr()),
+        vc_hip_colsum* pending = nullptr;
+        check(vc_hip_matmul_relu_mask_colsum_pending(dptr(a, a_offset), dptr(b, b_offset), out->ptr(), m, k, n,
+                                                     trans_a ? 1 : 0, trans_b ? 1 : 0, dptr(mask, mask_offset),
+                                                     sums->ptr(), &pending),
               "HIP matmul failed");
+        if (pending) sums->set_pending_sums(pending);
         out->set_column_sum(std::move(sums), m, n);
         return out;
     }
@@ -818,6 +878,9 @@ std::shared_ptr<Storage> HipBackend::reduce_axis(const Storage& input, std::size
     require(*this);
     if (length == 0 && operation != cpu::ReduceOp::Sum)
         throw std::invalid_argument("max/argmax over an empty axis is undefined");
+    // Row argmax the cross-entropy forward already computed from these rows.
+    if (operation == cpu::ReduceOp::Argmax && inner == 1)
+        if (auto indices = as_hip(input).take_row_argmax(offset, outer, length)) return indices;
     if (operation == cpu::ReduceOp::Sum && outer == 1 && offset == 0) {
         // Column sums the kernel that wrote the input already produced.
         if (auto sums = as_hip(input).take_column_sum(length, inner)) return sums;
@@ -862,6 +925,7 @@ void HipBackend::axpy_batch(const std::vector<AxpyItem>& items, float alpha) {
     std::vector<std::shared_ptr<const HipStorage>> current;  // kept alive until the launch is enqueued
     std::vector<float*> outputs;
     std::vector<const float*> targets, sources;
+    std::vector<const vc_hip_colsum*> sums;
     std::vector<std::size_t> counts;
     for (const AxpyItem& it : items) {
         auto& t = as_hip(*it.target);
@@ -869,16 +933,24 @@ void HipBackend::axpy_batch(const std::vector<AxpyItem>& items, float alpha) {
         if (it.count == 0) continue;
         outputs.push_back(t.ptr() + it.target_offset);
         targets.push_back(current.back()->ptr() + it.target_offset);
+        // A gradient that is still pending column sums (a bias gradient no
+        // one has read) is finished inside the update itself.
+        const vc_hip_colsum* pending = nullptr;
+        if (it.source != it.target && it.source_offset == 0 && it.count == it.source->size())
+            pending = as_hip(*it.source).pending_sums();
+        sums.push_back(pending);
         // A source in the target's own storage (a gradient that aliases its
         // parameter, e.g. from w.backward(w)) is read from the buffer holding
         // the current contents: before_write may have given the target a
         // fresh, unwritten buffer.
-        sources.push_back(it.source == it.target ? current.back()->ptr() + it.source_offset
-                                                 : dptr(*it.source, it.source_offset));
+        sources.push_back(pending ? nullptr
+                          : it.source == it.target ? current.back()->ptr() + it.source_offset
+                                                   : dptr(*it.source, it.source_offset));
         counts.push_back(it.count);
     }
     if (outputs.empty()) return;
-    check(vc_hip_axpy_batch(outputs.data(), targets.data(), sources.data(), counts.data(), outputs.size(), alpha),
+    check(vc_hip_axpy_batch_colsum(outputs.data(), targets.data(), sources.data(), sums.data(), counts.data(),
+                                   outputs.size(), alpha),
           "HIP axpy failed");
 }
 
@@ -1123,14 +1195,19 @@ std::pair<std::shared_ptr<Storage>, std::shared_ptr<Storage>> HipBackend::cross_
     require(*this);
     auto loss = fresh(1);
     auto stats = fresh(2 * rows);
+    // The forward also leaves each row's argmax (rows floats), kept with the
+    // logits for an argmax(1) of the unchanged logits: it then costs no
+    // second read of them.
+    auto indices = fresh(rows);
     // The loss is published as it is computed: loss.item() then waits for the
     // forward only, not the backward and update after it.
     vc_hip_mirror* published = nullptr;
-    check(vc_hip_xent_forward_published(dptr(logits, logits_offset),
-                                        reinterpret_cast<const std::int32_t*>(as_hip(targets).ptr()), rows, classes,
-                                        stats->ptr(), loss->ptr(), &published),
+    check(vc_hip_xent_forward_argmax(dptr(logits, logits_offset),
+                                     reinterpret_cast<const std::int32_t*>(as_hip(targets).ptr()), rows, classes,
+                                     stats->ptr(), loss->ptr(), indices->ptr(), &published),
           "HIP cross-entropy failed");
     loss->adopt_mirror(published);
+    as_hip(logits).set_row_argmax(std::move(indices), logits_offset, rows, classes);
     return {loss, stats};
 }
 
@@ -1145,10 +1222,12 @@ std::shared_ptr<Storage> HipBackend::cross_entropy_backward(const Storage& logit
     const std::optional<float> seed = grad_offset == 0 ? hip_host_scalar(grad_loss) : std::nullopt;
     if (column_sum && classes > 0) {
         auto sums = fresh(classes);
-        check(vc_hip_xent_backward_colsum(dptr(logits, logits_offset), t, as_hip(row_stats).ptr(),
-                                          seed ? nullptr : dptr(grad_loss, grad_offset), seed ? *seed : 0.0F, rows,
-                                          classes, out->ptr(), sums->ptr()),
+        vc_hip_colsum* pending = nullptr;
+        check(vc_hip_xent_backward_colsum_pending(dptr(logits, logits_offset), t, as_hip(row_stats).ptr(),
+                                                  seed ? nullptr : dptr(grad_loss, grad_offset), seed ? *seed : 0.0F,
+                                                  rows, classes, out->ptr(), sums->ptr(), &pending),
               "HIP cross-entropy backward failed");
+        if (pending) sums->set_pending_sums(pending);
         out->set_column_sum(std::move(sums), rows, classes);
         return out;
     }

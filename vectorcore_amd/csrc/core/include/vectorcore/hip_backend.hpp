@@ -80,6 +80,14 @@ public:
     };
     void axpy_batch(const std::vector<AxpyItem>& items, float alpha);
     void synchronize();
+    // download() of a published one-element result (a loss or a full sum)
+    // normally waits for its producer only, so item() can return while later
+    // work still runs. Strict mode restores the reference's contract
+    // (metal_backend.mm:198-211): every download first waits for the whole
+    // stream and reports any asynchronous failure. Off by default;
+    // VECTORCORE_HIP_STRICT_ITEM=1 or set_strict_item(true) turns it on.
+    void set_strict_item(bool enable);
+    [[nodiscard]] bool strict_item() const;
 
     // --- deferred forward products ---
     // A 2-D product A [m, k] @ B [k, n] (contiguous) can be recorded instead of

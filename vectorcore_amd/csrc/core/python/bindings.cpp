@@ -252,6 +252,18 @@ PYBIND11_MODULE(_vectorcore, m) {
         "Whether 2-D hip products are computed on first use (fusing a following bias add and ReLU); "
         "sets it when `enable` is given and returns the previous setting.");
     m.def(
+        "hip_strict_item",
+        [](std::optional<bool> enable) {
+            auto& b = HipBackend::instance();
+            const bool previous = b.strict_item();
+            if (enable) b.set_strict_item(*enable);
+            return previous;
+        },
+        py::arg("enable") = py::none(),
+        "Whether item()/to_vector() of a hip tensor first waits for all queued work and reports any asynchronous "
+        "failure, as the reference's download does (otherwise a published loss waits for its producer only); "
+        "sets it when `enable` is given and returns the previous setting.");
+    m.def(
         "hip_fuse_elementwise",
         [](std::optional<bool> enable) {
             auto& b = HipBackend::instance();

@@ -9,9 +9,12 @@
 // reference's CPU kernels (src/cpu/cpu_backend.cpp:24-27, 291-316); the build
 // disables floating-point contraction, so no fused multiply-add changes a
 // rounding.
+#include "reduce_common.hpp"
 #include "vc_hip_internal.hpp"
 
 #include <algorithm>
+#include <limits>
+#include <string>
 
 namespace vchip {
 namespace {
@@ -19,6 +22,7 @@ namespace {
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr unsigned kBlock = 256;
+constexpr int kWave = 64;
 
 __device__ inline f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 __device__ inline void st4(float* p, f4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p)); }
@@ -124,22 +128,61 @@ __global__ __launch_bounds__(kBlock) void map2_kernel(const float* __restrict__ 
 // The tensors are laid end to end in 16-byte chunks (first[k] = chunks before
 // tensor k); a thread finds its tensor by a short scan. Each tensor's last
 // chunk may be partial.
+//
+// A tensor whose gradient is still a set of pending column sums (part[k]:
+// part_rows[k] partial rows of count[k] doubles, see red::combine_waves) has
+// no chunks; instead the first blocks of the grid finish those sums, 64
+// columns per block, and update the tensor with them: four waves stand in for
+// the 16 virtual waves of the fixed order (wave w takes w, w + 4, w + 8,
+// w + 12), so the gradient has the bits red::column_partials_kernel gives it.
+// These blocks come first so that their load round trips overlap the stream.
 constexpr int kAxpyList = 16;
 struct AxpyList {
     float* o[kAxpyList];
     const float* t[kAxpyList];
     const float* s[kAxpyList];
+    const double* part[kAxpyList];
+    int64_t part_rows[kAxpyList];
     int64_t count[kAxpyList];
     int64_t first[kAxpyList + 1];
+    int combine_first[kAxpyList + 1];  // combine blocks before tensor k
     int n;
     float alpha;
 };
 
+constexpr int kCombineWavesPerBlock = kBlock / kWave;
+constexpr int kVirtualPerWave = red::kCombineWaves / kCombineWavesPerBlock;
+
 __global__ __launch_bounds__(kBlock) void axpy_list_kernel(AxpyList L) {
-    const int64_t total = L.first[L.n];
-    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
     const AxpyOp f{L.alpha};
-    for (int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; c < total; c += stride) {
+    const int combine_blocks = L.combine_first[L.n];
+    if (int(blockIdx.x) < combine_blocks) {
+        __shared__ double wave_sum[red::kCombineWaves][kWave];
+        int k = 0;
+        while (int(blockIdx.x) >= L.combine_first[k + 1]) ++k;
+        const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+        const int64_t col = int64_t(int(blockIdx.x) - L.combine_first[k]) * kWave + lane;
+        double acc[kVirtualPerWave];
+        if (col < L.count[k]) {
+            red::combine_waves<kVirtualPerWave>(L.part[k], L.part_rows[k], L.count[k], col, w, kCombineWavesPerBlock,
+                                                acc);
+        } else {
+#pragma unroll
+            for (int i = 0; i < kVirtualPerWave; ++i) acc[i] = 0.0;
+        }
+#pragma unroll
+        for (int i = 0; i < kVirtualPerWave; ++i) wave_sum[w + i * kCombineWavesPerBlock][lane] = acc[i];
+        __syncthreads();
+        if (w == 0 && col < L.count[k]) {
+            double total = wave_sum[0][lane];
+            for (int v = 1; v < red::kCombineWaves; ++v) total += wave_sum[v][lane];
+            L.o[k][col] = f(L.t[k][col], float(total));
+        }
+        return;
+    }
+    const int64_t total = L.first[L.n];
+    const int64_t stride = int64_t(gridDim.x - combine_blocks) * blockDim.x;
+    for (int64_t c = int64_t(blockIdx.x - combine_blocks) * blockDim.x + threadIdx.x; c < total; c += stride) {
         int k = 0;
         while (c >= L.first[k + 1]) ++k;
         const int64_t e = (c - L.first[k]) * 4;
@@ -410,6 +453,11 @@ int vc_hip_axpy(float* target, const float* source, size_t count, float alpha) {
 
 int vc_hip_axpy_batch(float* const* outputs, const float* const* targets, const float* const* sources,
                       const size_t* counts, size_t tensors, float alpha) {
+    return vc_hip_axpy_batch_colsum(outputs, targets, sources, nullptr, counts, tensors, alpha);
+}
+
+int vc_hip_axpy_batch_colsum(float* const* outputs, const float* const* targets, const float* const* sources,
+                             const vc_hip_colsum* const* sums, const size_t* counts, size_t tensors, float alpha) {
     return guard([&] {
         Device& d = require_device();
         if (tensors > 0 && (!outputs || !targets || !sources || !counts))
@@ -418,27 +466,50 @@ int vc_hip_axpy_batch(float* const* outputs, const float* const* targets, const 
         while (i < tensors) {
             AxpyList L{};
             double bytes = 0.0;
-            // Up to kAxpyList 16-byte-aligned tensors per launch; any other
-            // tensor goes through the single-tensor kernel on its own.
+            int64_t stream_chunks = 0;
+            // Up to kAxpyList tensors per launch: pending column sums, and
+            // 16-byte-aligned tensors; any other tensor goes through the
+            // single-tensor kernel on its own.
             for (; i < tensors && L.n < kAxpyList; ++i) {
                 if (counts[i] == 0) continue;
-                if (!outputs[i] || !targets[i] || !sources[i]) fail(VC_HIP_ERR_INVALID_ARGUMENT, "axpy_batch: null buffer");
-                if (!aligned16(outputs[i]) || !aligned16(targets[i]) || !aligned16(sources[i])) {
-                    launch_map2("axpy", targets[i], sources[i], outputs[i], counts[i], AxpyOp{alpha}, 12.0);
-                    continue;
+                const vc_hip_colsum* pending = sums ? sums[i] : nullptr;
+                if (!outputs[i] || !targets[i] || (!pending && !sources[i]))
+                    fail(VC_HIP_ERR_INVALID_ARGUMENT, "axpy_batch: null buffer");
+                if (pending) {
+                    if (int64_t(counts[i]) != pending->n)
+                        fail(VC_HIP_ERR_INVALID_ARGUMENT, "axpy_batch: pending column sums of " +
+                                                              std::to_string(pending->n) + " columns for a tensor of " +
+                                                              std::to_string(counts[i]));
+                    const int64_t blocks = (pending->n + kWave - 1) / kWave;
+                    if (int64_t(L.combine_first[L.n]) + blocks > std::numeric_limits<int>::max() / 2)
+                        fail(VC_HIP_ERR_OVERFLOW, "axpy_batch: too many pending columns");
+                    L.part[L.n] = pending->part;
+                    L.part_rows[L.n] = pending->rows;
+                    L.combine_first[L.n + 1] = L.combine_first[L.n] + int(blocks);
+                    L.first[L.n + 1] = L.first[L.n];
+                    bytes += 8.0 * double(pending->rows * pending->n) + 8.0 * double(counts[i]);
+                } else {
+                    if (!aligned16(outputs[i]) || !aligned16(targets[i]) || !aligned16(sources[i])) {
+                        launch_map2("axpy", targets[i], sources[i], outputs[i], counts[i], AxpyOp{alpha}, 12.0);
+                        continue;
+                    }
+                    L.s[L.n] = sources[i];
+                    L.combine_first[L.n + 1] = L.combine_first[L.n];
+                    L.first[L.n + 1] = L.first[L.n] + int64_t((counts[i] + 3) / 4);
+                    bytes += 12.0 * double(counts[i]);
                 }
                 L.o[L.n] = outputs[i];
                 L.t[L.n] = targets[i];
-                L.s[L.n] = sources[i];
                 L.count[L.n] = int64_t(counts[i]);
-                L.first[L.n + 1] = L.first[L.n] + int64_t((counts[i] + 3) / 4);
-                bytes += 12.0 * double(counts[i]);
+                stream_chunks = L.first[L.n + 1];
                 ++L.n;
             }
             if (L.n == 0) continue;
             L.alpha = alpha;
+            const unsigned stream_blocks = stream_chunks ? stream_grid(size_t(stream_chunks)) : 0u;
             Profiled p("axpy", 0.0, bytes);
-            launch(axpy_list_kernel, dim3(stream_grid(size_t(L.first[L.n]))), dim3(kBlock), 0, d.stream, L);
+            launch(axpy_list_kernel, dim3(unsigned(L.combine_first[L.n]) + stream_blocks), dim3(kBlock), 0, d.stream,
+                   L);
             after_launch("axpy");
             p.done();
         }

@@ -174,8 +174,7 @@ int vc_hip_map(const vc_hip_map_program* program) {
                       8.0 * double(p.n_sums) * double(g.gy * cols) + 4.0 * double(p.n_sums * cols));
         for (size_t s = 0; s < p.n_sums; ++s) {
             launch(red::column_partials_kernel, dim3(unsigned((cols + 63) / 64)), dim3(64 * red::kCombineWaves), 0,
-                   d.stream, part.as<double>() + int64_t(s) * g.gy * cols, g.gy,
-                   static_cast<const float*>(nullptr), rows, rows, cols, p.sums[s]);
+                   d.stream, part.as<double>() + int64_t(s) * g.gy * cols, g.gy, cols, p.sums[s]);
             after_launch("column_sum_combine");
         }
         prof.done();

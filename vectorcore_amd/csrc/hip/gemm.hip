@@ -75,8 +75,9 @@ struct GemmArgs {
     const float* relu_mask;        // null, or [batch][M][N]: C *= [relu_mask > 0] (fused ReLU backward)
     const float* bias;             // null, or [N]: C += bias[column] (fused row-bias add)
     int relu;                      // nonzero: C = C > 0 ? C : 0 after the bias (fused ReLU forward)
-    double* col_part;              // null, or [2 * (M / 128)][N] (batch 1, no split): column sums of the
-                                   //   final C values of each 64 rows of a full tile, in double
+    double* col_part;              // null, or partial rows of C's column sums (batch 1, no split), in
+                                   //   double: MFMA kernel 2 tiles_m rows (one per 64 rows of a tile),
+                                   //   FMA kernel tiles_m rows (one per 16-row tile)
 };
 
 // The forward epilogue, in the order of the unfused ops: the row-broadcast add
@@ -411,14 +412,15 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
                         acc[i][j][v] = bias_relu(value, bias[j], p.relu != 0);
                     }
         }
-        if (p.col_part && row_lim >= BM) {
-            // Column sums of a full tile's final values, in double, one partial
+        if (p.col_part) {
+            // Column sums of the tile's final values, in double, one partial
             // row per wave row (64 rows): each lane adds its 32 rows of a
             // column (i, then v), then the two half-waves (rows 4 apart) are
-            // joined. Partial row 2 tm + wm / 64. The rows of a last, partial
-            // tile are summed from C by column_partials_kernel instead, so no
-            // row needs a bounds check here.
+            // joined. Partial row 2 tm + wm / 64. In a last, partial tile the
+            // rows past M are left out (their values are not C's: a zero row
+            // of A times an infinite B is NaN).
             const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.col_part + (int64_t(2 * tm) + (wm >> 6)) * p.N + n0);
+            const bool whole = row_lim >= BM;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 double sum = 0.0;
@@ -427,7 +429,8 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
                         const float value = acc[i][j][v];
-                        sum += double(value);
+                        const int row = row0 + 32 * i + 8 * (v >> 2) + (v & 3);
+                        sum += whole || row < row_lim ? double(value) : 0.0;
                     }
                 sum += __shfl_xor(sum, 32, 64);
                 const int col = wn + 32 * j + (lane & 31);
@@ -616,11 +619,24 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
                 __syncthreads();
             }
         }
-        if (row < p.M && col < p.N) {
+        const bool inside = row < p.M && col < p.N;
+        if (inside) {
             const int64_t t = z * p.M * p.N + row * p.N + col;
             if (p.relu_mask) acc = acc * (p.relu_mask[t] > 0.0f ? 1.0f : 0.0f);
             if (p.bias || p.relu) acc = bias_relu(acc, p.bias ? p.bias[col] : 0.0f, p.relu != 0);
             p.c[t] = acc;
+        }
+        if (p.col_part) {  // batch 1: the tile's 16 rows of each column, in row order, in double
+            __shared__ double tile_rows[16][16];
+            tile_rows[ty][tx] = inside ? double(acc) : 0.0;
+            __syncthreads();
+            if (ty == 0 && col < p.N) {
+                double sum = 0.0;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sum += tile_rows[r][tx];
+                p.col_part[(row0 / 16) * p.N + col] = sum;
+            }
+            __syncthreads();
         }
     }
 }
@@ -646,11 +662,13 @@ const char* variant_label(bool ta, bool tb) {
 void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t a_bstride,
           int64_t b_bstride, const std::vector<int64_t>* offsets, int64_t reduce, int64_t a_rstride, int64_t b_rstride,
           bool ta, bool tb, const float* relu_mask = nullptr, const float* bias = nullptr, bool relu = false,
-          bool in_caller_scope = false, float* column_sum = nullptr) {
+          bool in_caller_scope = false, float* column_sum = nullptr, vc_hip_colsum** pending = nullptr) {
     Device& d = require_device();
     if (M < 0 || N < 0 || K < 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "negative matrix dimension");
+    if (pending) *pending = nullptr;
     if (column_sum && (batch != 1 || reduce != 1))
         fail(VC_HIP_ERR_INVALID_ARGUMENT, "a fused column sum needs a single product");
+    if (pending && !column_sum) fail(VC_HIP_ERR_INVALID_ARGUMENT, "pending column sums need a column-sum buffer");
     if (M == 0 || N == 0 || batch == 0) return;
     if (!a || !b || !c) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul: null buffer");
     const bool force_simple = d.simple_gemm.load();  // the kernel in force for this call
@@ -668,7 +686,8 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
                bt.as<float>(), K, N);
         after_launch("gemm_nn");
         // Inside this scope: the transpose and the product are timed together.
-        gemm(a, bt.as<float>(), c, M, N, K, 1, 0, 0, nullptr, 1, 0, 0, false, true, nullptr, bias, relu, true);
+        gemm(a, bt.as<float>(), c, M, N, K, 1, 0, 0, nullptr, 1, 0, 0, false, true, nullptr, bias, relu, true,
+             column_sum, pending);
         prof.done();
         return;
     }
@@ -756,13 +775,14 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     args.relu_mask = relu_mask;
     args.bias = bias;
     args.relu = relu ? 1 : 0;
-    // The column sum of C (a bias gradient) comes from the epilogue's per-tile
-    // partials when one MFMA launch writes C; otherwise it is a separate
-    // axis reduction of C afterwards.
-    const bool epilogue_sums = column_sum && !simple && splits == 1;
-    const int64_t full_tiles = M / BM;
-    Scratch col_part(epilogue_sums && full_tiles ? size_t(2 * full_tiles) * size_t(N) * sizeof(double) : 8);
-    if (epilogue_sums) args.col_part = col_part.as<double>();
+    // The column sums of C (a bias gradient) come from partial rows that the
+    // epilogue keeps when one launch writes C (the MFMA kernel one per 64 rows
+    // of a tile, the FMA kernel one per 16-row tile): column_partials_kernel
+    // adds them next, or they are handed to the caller as pending sums. A
+    // split product's C is summed again afterwards instead.
+    ColsumPtr sums;
+    if (column_sum && splits == 1) sums = new_colsum(simple ? tiles_m_simple : 2 * tiles_m, N);
+    if (sums) args.col_part = sums->part;
     const double bytes =
         4.0 * (double(M * K + K * N) * double(reduce) + double(M * N) * (relu_mask ? 2.0 : 1.0)) * double(batch) +
         (bias ? 4.0 * double(N) : 0.0);
@@ -781,14 +801,9 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     }
     after_launch(label);
     if (prof) prof->done();
-    if (epilogue_sums) {
-        Profiled pc("column_sum_combine", 0.0,
-                    8.0 * double(2 * full_tiles) * double(N) + 4.0 * double(M - full_tiles * BM + 1) * double(N));
-        launch(red::column_partials_kernel, dim3(unsigned((N + 63) / 64)), dim3(64 * red::kCombineWaves), 0, d.stream,
-               col_part.as<double>(),
-               2 * full_tiles, static_cast<const float*>(c), full_tiles * BM, M, N, column_sum);
-        after_launch("column_sum_combine");
-        pc.done();
+    if (sums) {
+        if (pending) *pending = sums.release();
+        else finish_colsum(*sums, column_sum);
     } else if (column_sum) {
         const int rc = vc_hip_reduce_axis(c, column_sum, 1, size_t(M), size_t(N), VC_REDUCE_SUM);
         if (rc != VC_HIP_OK) fail(rc, std::string("column sum of a product: ") + vc_hip_last_error());
@@ -841,19 +856,38 @@ int vc_hip_matmul_relu_mask(const float* a, const float* b, float* c, size_t m, 
     });
 }
 
+}  // extern "C"
+
+namespace {
+void relu_mask_colsum(const float* a, const float* b, float* c, size_t m, size_t k, size_t n, int trans_a,
+                      int trans_b, const float* mask, float* column_sum, vc_hip_colsum** pending) {
+    if (pending) *pending = nullptr;
+    if (!mask || !column_sum) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask_colsum: null mask or column sum");
+    if (n == 0) return;
+    if (m == 0) {  // an empty column sum is zero
+        const int rc = vc_hip_fill(column_sum, n, 0.0f);
+        if (rc != VC_HIP_OK) fail(rc, vc_hip_last_error());
+        return;
+    }
+    if (k == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask_colsum needs k > 0");
+    gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), 1, 0, 0, nullptr, 1, 0, 0, trans_a != 0, trans_b != 0, mask,
+         nullptr, false, false, column_sum, pending);
+}
+}  // namespace
+
+extern "C" {
+
 int vc_hip_matmul_relu_mask_colsum(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
                                    int trans_a, int trans_b, const float* mask, float* column_sum) {
+    return guard([&] { relu_mask_colsum(a, b, c, m, k, n, trans_a, trans_b, mask, column_sum, nullptr); });
+}
+
+int vc_hip_matmul_relu_mask_colsum_pending(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                                           int trans_a, int trans_b, const float* mask, float* column_sum,
+                                           vc_hip_colsum** pending) {
     return guard([&] {
-        if (!mask || !column_sum) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask_colsum: null mask or column sum");
-        if (n == 0) return;
-        if (m == 0) {  // an empty column sum is zero
-            const int rc = vc_hip_fill(column_sum, n, 0.0f);
-            if (rc != VC_HIP_OK) fail(rc, vc_hip_last_error());
-            return;
-        }
-        if (k == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask_colsum needs k > 0");
-        gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), 1, 0, 0, nullptr, 1, 0, 0, trans_a != 0, trans_b != 0, mask,
-             nullptr, false, false, column_sum);
+        if (!pending) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask_colsum_pending: null handle pointer");
+        relu_mask_colsum(a, b, c, m, k, n, trans_a, trans_b, mask, column_sum, pending);
     });
 }
 

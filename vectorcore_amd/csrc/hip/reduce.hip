@@ -333,7 +333,7 @@ __global__ __launch_bounds__(kBlock) void colsum_finish_kernel(const float* __re
         // A device-scope store is acknowledged once it is visible at device
         // scope: waiting for every outstanding memory operation orders these
         // stores before the count below.
-        __builtin_amdgcn_s_waitcnt(0);
+        red::wait_stores_visible();
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -650,7 +650,10 @@ void reduce_axis(const float* in, float* out, int64_t outer, int64_t len, int64_
     }
     if (op == VC_REDUCE_SUM) {
         const ColumnPlan c = column_plan(in, outer, len, inner);
-        double* part = static_cast<double*>(memory.take(size_t(c.segs * total) * sizeof(double)));
+        // One segment: colsum_tile_kernel writes the sums directly and never
+        // touches partials, so none are taken.
+        double* part =
+            c.segs > 1 ? static_cast<double*>(memory.take(size_t(c.segs * total) * sizeof(double))) : nullptr;
         column_sum(d, c, in, out, part, outer, len, inner, label);
         p.done();
         return;
@@ -728,6 +731,28 @@ private:
 };
 
 }  // namespace
+
+void ColsumRelease::operator()(vc_hip_colsum* h) const noexcept {
+    if (!h) return;
+    pool_release(h->part);
+    delete h;
+}
+
+ColsumPtr new_colsum(int64_t rows, int64_t n) {
+    if (rows <= 0 || n <= 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "pending column sums need at least one row and column");
+    void* part = pool_alloc(size_t(rows) * size_t(n) * sizeof(double));
+    return ColsumPtr(new vc_hip_colsum{static_cast<double*>(part), rows, n});
+}
+
+void finish_colsum(const vc_hip_colsum& h, float* out) {
+    Device& d = require_device();
+    Profiled p("column_sum_combine", 0.0, 8.0 * double(h.rows * h.n) + 4.0 * double(h.n));
+    launch(red::column_partials_kernel, dim3(unsigned((h.n + 63) / 64)), dim3(64 * red::kCombineWaves), 0, d.stream,
+           static_cast<const double*>(h.part), h.rows, h.n, out);
+    after_launch("column_sum_combine");
+    p.done();
+}
+
 }  // namespace vchip
 
 using namespace vchip;
@@ -801,6 +826,24 @@ int vc_hip_transpose_last2(const float* in, float* out, size_t batch, size_t row
         after_launch("transpose_last2");
         p.done();
     });
+}
+
+int vc_hip_colsum_finish(const vc_hip_colsum* sums, float* column_sum) {
+    return guard([&] {
+        if (!sums || !column_sum) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_colsum_finish: null pointer");
+        finish_colsum(*sums, column_sum);
+    });
+}
+
+int vc_hip_colsum_size(const vc_hip_colsum* sums, size_t* columns) {
+    return guard([&] {
+        if (!sums || !columns) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_colsum_size: null pointer");
+        *columns = size_t(sums->n);
+    });
+}
+
+int vc_hip_colsum_release(vc_hip_colsum* sums) {
+    return guard([&] { ColsumRelease()(sums); });
 }
 
 }  // extern "C"

@@ -194,6 +194,21 @@ __device__ inline double chunk_sum(const float* __restrict__ x, int64_t b0, int6
 // block is last, and it resets the top counter for the next launch. Launches
 // on the library's one stream never overlap, so each translation unit's
 // counters (static, zero at load) serve all its one-launch kernels.
+
+// The wait that orders a block's partial stores before its counter atomic.
+// The ordering in hardware comes from s_waitcnt 0, which waits until every
+// store of this wave is acknowledged; an agent-scope store (sc1) is
+// acknowledged only once it is visible at agent scope, and the finishing
+// block reads the partials with sc1 loads, which read that coherent copy. The
+// wait builtin alone does not stop the compiler from moving the relaxed
+// atomics around it, so compiler-only fences (no instruction is emitted)
+// keep the stores before it and the counter atomic after it.
+__device__ inline void wait_stores_visible() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 constexpr unsigned kDoneGroup = 64, kDoneGroups = 64, kDoneStride = 32;
 constexpr unsigned kMaxFinishBlocks = kDoneGroup * kDoneGroups;
 static __device__ unsigned int g_group_done[kDoneGroups * kDoneStride];
@@ -205,14 +220,14 @@ __device__ inline bool count_in(double block_partial, double* __restrict__ part)
     __shared__ int last_block;
     if (threadIdx.x == 0) {
         __hip_atomic_store(&part[blockIdx.x], block_partial, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
+        wait_stores_visible();
         const unsigned group = blockIdx.x / kDoneGroup, groups = (gridDim.x + kDoneGroup - 1) / kDoneGroup;
         const unsigned members = min(kDoneGroup, gridDim.x - group * kDoneGroup);
         unsigned* counter = &g_group_done[group * kDoneStride];
         bool last = false;
         if (__hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == members) {
             __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_s_waitcnt(0);
+            wait_stores_visible();
             last = __hip_atomic_fetch_add(&g_groups_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == groups;
         }
         last_block = last;
@@ -291,33 +306,52 @@ __global__ __launch_bounds__(kBlock) void sum_final_kernel(const double* __restr
     if (threadIdx.x == 0) out[0] = finish(float(total));
 }
 
-// out[col] = float(column sum) from partial rows written by a producing
-// kernel (part, `rows` rows of n doubles) and, for rows r >= c_row0 of the
-// producer's output C that no partial covers, from C itself. A workgroup takes 64
-// columns with 16 waves; wave w sums, for its lane's column, the partial rows
-// t = w, w + 16, ... and then the C rows c_row0 + w, c_row0 + w + 16, ... in
-// double, and the 16 wave sums are added in wave order: a fixed order.
+// ---- column sums from a producer's partial rows ---------------------------
+// A kernel that writes a matrix can leave `rows` partial rows of its column
+// sums (n doubles each, every row of the matrix in exactly one). The column
+// sum is then added in one fixed order: "virtual wave" w of kCombineWaves
+// adds the partial rows t = w, w + 16, w + 32, ... in ascending order, and the
+// 16 wave sums are added in wave order, then rounded once to float. Every
+// kernel that finishes such sums (column_partials_kernel, the SGD list
+// kernel's combine blocks) takes them from combine_waves, so a column's sum
+// has the same bits whichever kernel adds it.
 constexpr int kCombineWaves = 16;
-static __global__ __launch_bounds__(64 * kCombineWaves) void column_partials_kernel(
-    const double* __restrict__ part, int64_t rows, const float* __restrict__ c, int64_t c_row0, int64_t m, int64_t n,
-    float* __restrict__ out) {
+
+// acc[i] = the sum of virtual wave w0 + i * wstep for column col (V virtual
+// waves at once, eight loads in flight per wave).
+template <int V>
+__device__ inline void combine_waves(const double* __restrict__ part, int64_t rows, int64_t n, int64_t col, int w0,
+                                     int wstep, double (&acc)[V]) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0;
+    for (int64_t t0 = 0; t0 < rows; t0 += 8 * kCombineWaves) {
+        double v[V][8];
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t t = t0 + w0 + i * wstep + u * kCombineWaves;
+                v[i][u] = t < rows ? part[t * n + col] : 0.0;
+            }
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (t0 + w0 + i * wstep + u * kCombineWaves < rows) acc[i] += v[i][u];
+    }
+}
+
+// out[col] = float(column sum) of `rows` partial rows: a workgroup takes 64
+// columns with one wave per virtual wave.
+static __global__ __launch_bounds__(64 * kCombineWaves) void column_partials_kernel(const double* __restrict__ part,
+                                                                                   int64_t rows, int64_t n,
+                                                                                   float* __restrict__ out) {
     __shared__ double wave_sum[kCombineWaves][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t col = int64_t(blockIdx.x) * 64 + lane;
-    double acc = 0.0;
-    if (col < n) {
-        int64_t t = w;
-        for (; t + 7 * kCombineWaves < rows; t += 8 * kCombineWaves) {  // eight loads in flight
-            double v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = part[(t + u * kCombineWaves) * n + col];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc += v[u];
-        }
-        for (; t < rows; t += kCombineWaves) acc += part[t * n + col];
-        for (int64_t r = c_row0 + w; r < m; r += kCombineWaves) acc += double(c[r * n + col]);
-    }
-    wave_sum[w][lane] = acc;
+    double acc[1] = {0.0};
+    if (col < n) combine_waves<1>(part, rows, n, col, w, 0, acc);
+    wave_sum[w][lane] = acc[0];
     __syncthreads();
     if (w == 0 && col < n) {
         double total = wave_sum[0][lane];

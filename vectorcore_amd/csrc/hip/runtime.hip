@@ -622,6 +622,20 @@ int vc_hip_synchronize(void) {
     });
 }
 
+int vc_hip_stream_idle(int* idle) {
+    return guard([&] {
+        if (!idle) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_stream_idle: null pointer");
+        Device& d = device();
+        if (!d.ready) {
+            *idle = 1;
+            return;
+        }
+        const hipError_t state = hipStreamQuery(d.stream);
+        if (state != hipSuccess && state != hipErrorNotReady) check_hip(state, "HIP command failed");
+        *idle = state == hipSuccess ? 1 : 0;
+    });
+}
+
 int vc_hip_pool_stats_get(vc_hip_pool_stats* out) {
     return guard([&] {
         if (!out) fail(VC_HIP_ERR_INVALID_ARGUMENT, "null stats pointer");

@@ -9,6 +9,7 @@
 #include <atomic>
 #include <cstddef>
 #include <cstdint>
+#include <memory>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -21,6 +22,16 @@
 struct vc_hip_mirror {
     float* host;
     hipEvent_t done;
+};
+
+// Column sums left pending by the kernel that wrote a matrix: `rows` partial
+// rows of n doubles (every row of the matrix counted in exactly one) in a
+// pool buffer, added in red::combine_waves' order by whichever kernel
+// finishes them (vc_hip_colsum_finish, vc_hip_axpy_batch_colsum).
+struct vc_hip_colsum {
+    double* part;
+    int64_t rows;
+    int64_t n;
 };
 
 namespace vchip {
@@ -91,6 +102,17 @@ void pool_release(void* p) noexcept;
 vc_hip_mirror* take_mirror();
 void give_mirror(vc_hip_mirror* m) noexcept;
 void launch_mirror(vc_hip_mirror* m, const float* device_value);
+
+// Pending column sums (reduce.hip): a handle owning a pool buffer of
+// rows * n doubles, released in stream order; finish_colsum enqueues
+// column_partials_kernel into out (n floats) under the "column_sum_combine"
+// profiler label.
+struct ColsumRelease {
+    void operator()(vc_hip_colsum* h) const noexcept;
+};
+using ColsumPtr = std::unique_ptr<vc_hip_colsum, ColsumRelease>;
+ColsumPtr new_colsum(int64_t rows, int64_t n);
+void finish_colsum(const vc_hip_colsum& h, float* out);
 class Scratch {
 public:
     explicit Scratch(size_t bytes) : p_(pool_alloc(bytes)) {}

@@ -47,7 +47,10 @@ using red::kNone;
 // whichever path (register-held or streaming) it takes.
 __device__ inline float row_exp(float s) { return __expf(s); }
 
-__device__ inline float row_max(const float* row, int64_t len, int lane, bool vec) {
+// The row's maximum as the reference's max() takes it, and (in .i) its
+// argmax: the first strict maximum of an ascending scan, element 0 when that
+// is NaN or when no element is above -inf.
+__device__ inline Best row_max(const float* row, int64_t len, int lane, bool vec) {
     Best b = red::no_best();
     if (vec) {
         for (int64_t a = int64_t(lane) * 4; a < len; a += kWave * 4) {
@@ -62,7 +65,8 @@ __device__ inline float row_max(const float* row, int64_t len, int lane, bool ve
     }
     b = red::wave_best(b);
     const float first = row[0];
-    return first != first ? first : b.v;  // max() keeps a NaN first element (src/cpu/cpu_backend.cpp:443-452)
+    if (first != first) return Best{first, 0};  // max() keeps a NaN first element (src/cpu/cpu_backend.cpp:443-452)
+    return Best{b.v, b.i == kNone ? 0 : b.i};
 }
 
 // Lane 0: the row's statistics (max, exp-sum) and its loss term
@@ -116,6 +120,45 @@ __device__ inline uint32_t wave_umax(uint32_t v) {
 
 __device__ inline uint32_t bits_of(float v) { return __builtin_bit_cast(uint32_t, v); }
 
+// Smallest value over the wavefront (Steps 6) or each half-wave (Steps 5).
+template <int Steps>
+__device__ inline int lanes_min(int v) {
+    const int lane = red::lane_id();
+    v = min(v, red::partner<0>(v, lane));
+    v = min(v, red::partner<1>(v, lane));
+    v = min(v, red::partner<2>(v, lane));
+    v = min(v, red::partner<3>(v, lane));
+    v = min(v, red::partner<4>(v, lane));
+    if constexpr (Steps == 6) v = min(v, red::partner<5>(v, lane));
+    return v;
+}
+
+// The reference's argmax of a row (src/cpu/cpu_backend.cpp:443-457), from the
+// row's maximum m as the statistics take it: the first strict maximum of an
+// ascending scan is the first element equal to the largest non-NaN value (a
+// tie, ±0 included, never replaces the running best), and a NaN element 0 is
+// never replaced (m is then that NaN and no element equals it). So: the
+// smallest index holding a value == m, else 0. v holds NV float4 per lane,
+// element a = base + Stride u + component (padding past the row holds -inf,
+// which equals m only when a real element does, at a smaller index). Returns
+// this lane's smallest such index, kNone if none; the caller takes the
+// minimum over the row's lanes.
+template <int NV, int Stride>
+__device__ inline int first_equal(const f4 (&v)[NV], float m, int base) {
+    int idx = kNone;
+#pragma unroll
+    for (int u = NV - 1; u >= 0; --u) {  // descending, so the smallest index is written last
+        const int a = base + Stride * u;
+        idx = v[u].w == m ? a + 3 : idx;
+        idx = v[u].z == m ? a + 2 : idx;
+        idx = v[u].y == m ? a + 1 : idx;
+        idx = v[u].x == m ? a : idx;
+    }
+    return idx;
+}
+
+__device__ inline float argmax_value(int idx) { return float(idx == kNone ? 0 : idx); }
+
 // Row statistics and loss term of one row from values in registers (NV
 // float4 per lane; element a = 4 lane + 256 u + component, a row of at most
 // 256 NV classes; elements past the row hold -inf). Each lane visits its
@@ -123,7 +166,7 @@ __device__ inline uint32_t bits_of(float v) { return __builtin_bit_cast(uint32_t
 // same bits. Returns the loss term on lane 0.
 template <bool Vec, int NV>
 __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, int t, int lane,
-                                   float* __restrict__ stats) {
+                                   float* __restrict__ stats, float* __restrict__ amax) {
     // The reference's max is the first strict maximum, skipping NaN after
     // element 0. Its value is the largest non-NaN element, whichever index
     // holds it (fmaxf ignores NaN too), except for the sign of a zero maximum
@@ -170,6 +213,10 @@ __device__ inline float finish_row(const f4 (&v)[NV], int64_t r, int64_t len, in
         m = red::wave_best(b).v;
     } else {
         m = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, mx)));
+    }
+    if (amax) {
+        const int idx = lanes_min<6>(first_equal<NV, kWave * 4>(v, m, lane * 4));
+        if (lane == 0) amax[r] = argmax_value(idx);
     }
     // Elements past the row give exp(-inf - m) = 0 (or NaN when m is -inf or
     // NaN, and then every real element's term is NaN too): adding them leaves
@@ -356,7 +403,8 @@ __device__ inline void load_half_row(f4 (&v)[NV], const float* __restrict__ row,
 // with a half-wave's lanes.
 template <bool Vec, int NV>
 __device__ inline float finish_half_row(const f4 (&v)[NV], int64_t r, bool valid, const float* __restrict__ row,
-                                        int64_t len, int t, int lane, float* __restrict__ stats) {
+                                        int64_t len, int t, int lane, float* __restrict__ stats,
+                                        float* __restrict__ amax) {
     const int hl = lane & 31;
     const bool t_in_row = t >= 0 && int64_t(t) < len;
     const float x_t = t_in_row ? row[t] : 0.0f;  // loaded now, used at the end
@@ -398,6 +446,10 @@ __device__ inline float finish_half_row(const f4 (&v)[NV], int64_t r, bool valid
         m = half_best(b).v;
     } else {
         m = mx;
+    }
+    if (amax) {
+        const int idx = lanes_min<5>(first_equal<NV, 128>(v, m, hl * 4));
+        if (hl == 0 && valid) amax[r] = argmax_value(idx);
     }
     double c0 = 0.0, c1 = 0.0, c2 = 0.0, c3 = 0.0;  // as in finish_row
 #pragma unroll
@@ -458,13 +510,16 @@ __device__ inline void finish_loss(double* wave_terms, double* __restrict__ part
     }
 }
 
+// Rows of 1025 to 4096 classes. cur and next alone take 2 NV float4 per
+// lane (64 registers at NV 8, 128 at NV 16), so the allocation is left to the
+// compiler: any minimum of waves per SIMD (six, or four at NV 8 and two at
+// NV 16) made it spill to scratch.
 template <int NV, bool Vec>
-// Six waves per SIMD (at most 80 registers) fit without spilling and measured
-// 2-10% faster than the unconstrained allocation (4 waves); eight spill.
-__global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float* __restrict__ x,
+__global__ __launch_bounds__(kBlock) void xent_rows_cached_kernel(const float* __restrict__ x,
                                                                   const int* __restrict__ targets, int64_t rows,
                                                                   int64_t len, float* __restrict__ stats,
-                                                                  double* __restrict__ part, float* __restrict__ loss,
+                                                                  float* __restrict__ amax, double* __restrict__ part,
+                                                                  float* __restrict__ loss,
                                                                   float* __restrict__ host_loss) {
     __shared__ double wave_terms[kRowsPerBlock];
     const int lane = threadIdx.x % kWave;
@@ -487,7 +542,7 @@ __global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float
                 tn = targets[rn];
                 load_row<Vec>(next, x + rn * len, len, lane);
             }
-            total += double(finish_row<Vec>(cur, r, len, t, lane, stats));
+            total += double(finish_row<Vec>(cur, r, len, t, lane, stats, amax));
 #pragma unroll
             for (int u = 0; u < NV; ++u) cur[u] = next[u];
             t = __builtin_amdgcn_readfirstlane(tn);
@@ -501,15 +556,15 @@ __global__ __launch_bounds__(kBlock, 6) void xent_rows_cached_kernel(const float
 // takes row pairs p = w, w + W, ... (rows 2p and 2p + 1). The loss terms are
 // summed per half in row order, then the wavefront's lower half before its
 // upper half, then as xent_rows_cached_kernel does (its last block finishes
-// the loss). Five waves per SIMD (96 registers) fit without spilling and
-// measured faster than six (which spill) or loading the next pair ahead (three
-// waves): 32768 x 1000 in 22.8 us against 25.8 us for a row per wavefront.
+// the loss). With 16-byte loads five waves per SIMD (96 registers) fit without
+// spilling and measured faster than six (which spill) or loading the next pair
+// ahead (three waves): 32768 x 1000 in 22.8 us against 25.8 us for a row per
+// wavefront. The scalar-load variant (rows not a multiple of 4 classes, or
+// misaligned) needs a few more registers at NV 8 and runs four waves.
 template <int NV, bool Vec>
-__global__ __launch_bounds__(kBlock, 5) void xent_half_rows_kernel(const float* __restrict__ x,
-                                                                   const int* __restrict__ targets, int64_t rows,
-                                                                   int64_t len, float* __restrict__ stats,
-                                                                   double* __restrict__ part, float* __restrict__ loss,
-                                                                   float* __restrict__ host_loss) {
+__global__ __launch_bounds__(kBlock, Vec || NV < 8 ? 5 : 4) void xent_half_rows_kernel(
+    const float* __restrict__ x, const int* __restrict__ targets, int64_t rows, int64_t len, float* __restrict__ stats,
+    float* __restrict__ amax, double* __restrict__ part, float* __restrict__ loss, float* __restrict__ host_loss) {
     __shared__ double wave_terms[kRowsPerBlock];
     const int lane = threadIdx.x % kWave, h = lane >> 5;
     const int64_t wave_id = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
@@ -521,7 +576,7 @@ __global__ __launch_bounds__(kBlock, 5) void xent_half_rows_kernel(const float* 
         const int t = targets[rr];
         f4 v[NV];
         load_half_row<Vec>(v, x + rr * len, len, lane & 31);
-        total += double(finish_half_row<Vec>(v, rr, r < rows, x + rr * len, len, t, lane, stats));
+        total += double(finish_half_row<Vec>(v, rr, r < rows, x + rr * len, len, t, lane, stats, amax));
     }
     const uint64_t tb = __builtin_bit_cast(uint64_t, total);
     const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(tb)), 32));
@@ -536,13 +591,15 @@ __global__ __launch_bounds__(kBlock, 5) void xent_half_rows_kernel(const float* 
 template <bool Vec>
 __global__ __launch_bounds__(kBlock) void xent_rows_kernel(const float* __restrict__ x, const int* __restrict__ targets,
                                                            int64_t rows, int64_t len, float* __restrict__ stats,
-                                                           float* __restrict__ terms) {
+                                                           float* __restrict__ amax, float* __restrict__ terms) {
     const int lane = threadIdx.x % kWave;
     const int64_t r = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
     if (r >= rows) return;
     const float* row = x + r * len;
     const int t = targets[r];
-    const float m = row_max(row, len, lane, Vec);
+    const Best best = row_max(row, len, lane, Vec);
+    const float m = best.v;
+    if (amax && lane == 0) amax[r] = float(best.i);
     double acc = 0.0;
     int bad = 0;  // a non-target log-prob that is not finite
     if (Vec) {  // four component chains, joined in order, as the register-held path adds
@@ -723,9 +780,10 @@ void xent_backward(const float* logits, const int32_t* targets, const float* row
 // host slot: by the finishing block of a register-held row kernel, whose
 // dispatch then carries the mirror's completion event, or, when the profiler
 // holds the dispatch's events or the rows are streamed, by a copy launched
-// after the forward.
+// after the forward. With row_argmax, every path also writes each row's
+// argmax (as a float index) from the row it already holds.
 void xent_forward(const float* logits, const int32_t* targets, size_t rows, size_t classes, float* row_stats,
-                  float* loss, vc_hip_mirror* publish) {
+                  float* loss, float* row_argmax, vc_hip_mirror* publish) {
     Device& d = require_device();
     if (rows == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "cross_entropy of an empty batch is undefined");
     if (classes == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "cross_entropy needs at least one class");
@@ -734,7 +792,8 @@ void xent_forward(const float* logits, const int32_t* targets, size_t rows, size
     Scratch terms(rows * sizeof(float));
     const bool vec = C % 4 == 0 && aligned16(logits);
     const unsigned grid = unsigned((R + kRowsPerBlock - 1) / kRowsPerBlock);
-    Profiled p("xent_forward", 0.0, 4.0 * double(R * C) + 4.0 * double(R) + 8.0 * double(R));
+    Profiled p("xent_forward", 0.0,
+               4.0 * double(R * C) + 4.0 * double(R) + 8.0 * double(R) + (row_argmax ? 4.0 * double(R) : 0.0));
     // Rows are held in registers: up to 1024 classes two rows per wavefront,
     // up to 4096 one row per wavefront (NV float4 per lane); at most 8
     // workgroups per CU walk the rows (3 to 12 per CU measured within 3%).
@@ -757,9 +816,9 @@ void xent_forward(const float* logits, const int32_t* targets, size_t rows, size
     auto row_launch = [&](auto kernel, unsigned blocks) {
         if (published)
             hipExtLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlock), 0, d.stream, nullptr, published, 0u, logits,
-                                  targets, R, C, row_stats, part.as<double>(), loss, host_loss);
+                                  targets, R, C, row_stats, row_argmax, part.as<double>(), loss, host_loss);
         else
-            launch(kernel, dim3(blocks), dim3(kBlock), 0, d.stream, logits, targets, R, C, row_stats,
+            launch(kernel, dim3(blocks), dim3(kBlock), 0, d.stream, logits, targets, R, C, row_stats, row_argmax,
                    part.as<double>(), loss, host_loss);
     };
     const int64_t nh = (C + 127) / 128;  // float4s per lane with a half-wave per row
@@ -777,7 +836,7 @@ void xent_forward(const float* logits, const int32_t* targets, size_t rows, size
     } else if (nv > 16) {
         // Row terms, then the shared deterministic full sum (one launch).
         launch((vec ? xent_rows_kernel<true> : xent_rows_kernel<false>), dim3(grid), dim3(kBlock), 0, d.stream,
-               logits, targets, R, C, row_stats, terms.as<float>());
+               logits, targets, R, C, row_stats, row_argmax, terms.as<float>());
         after_launch("xent_forward");
         const int64_t chunk = red::sum_chunk(R);
         const int64_t blocks = (R + chunk - 1) / chunk;
@@ -797,6 +856,65 @@ void xent_forward(const float* logits, const int32_t* targets, size_t rows, size
     p.done();
 }
 
+// Runs forward(m) with a mirror taken for it, handed to *mirror on success.
+template <class F>
+void with_mirror(vc_hip_mirror** mirror, const char* name, F&& forward) {
+    if (!mirror) fail(VC_HIP_ERR_INVALID_ARGUMENT, std::string(name) + ": null mirror");
+    require_device();
+    vc_hip_mirror* m = take_mirror();
+    try {
+        forward(m);
+    } catch (...) {
+        give_mirror(m);
+        throw;
+    }
+    *mirror = m;
+}
+
+// The backward with the column sums of dx (vc_hip_xent_backward_colsum):
+// for rows of at most 2048 classes the kernel keeps one partial row per
+// kColRows rows, finished next by column_partials_kernel or, with `pending`,
+// handed to the caller; longer rows run the plain backward and a separate
+// reduction of dx.
+void xent_backward_colsum(const float* logits, const int32_t* targets, const float* row_stats, const float* grad_loss,
+                          float grad_loss_value, size_t rows, size_t classes, float* grad_logits, float* column_sum,
+                          vc_hip_colsum** pending) {
+    Device& d = require_device();
+    if (pending) *pending = nullptr;
+    if (!column_sum) fail(VC_HIP_ERR_INVALID_ARGUMENT, "xent_backward_colsum: null column sum");
+    if (classes == 0) return;
+    if (classes > size_t(std::numeric_limits<int>::max())) fail(VC_HIP_ERR_OVERFLOW, "too many classes");
+    const int64_t R = int64_t(rows), C = int64_t(classes);
+    const int64_t nv = (C + kWave * 4 - 1) / (kWave * 4);
+    const bool fused = rows > 0 && nv <= 8;
+    const bool vec = C % 4 == 0 && aligned16(logits) && aligned16(grad_logits);
+    if (!fused) {  // the plain backward, then a separate reduction of dx
+        xent_backward(logits, targets, row_stats, grad_loss, grad_loss_value, rows, classes, grad_logits);
+        const int rc = vc_hip_reduce_axis(grad_logits, column_sum, 1, rows, classes, VC_REDUCE_SUM);
+        if (rc != VC_HIP_OK) fail(rc, std::string("column sum of the cross-entropy gradient: ") + vc_hip_last_error());
+        return;
+    }
+    const int64_t blocks = (R + kColRows - 1) / kColRows;
+    if (blocks > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, "too many rows");
+    ColsumPtr sums = new_colsum(blocks, C);
+    {
+        Profiled p("xent_backward", 0.0, 8.0 * double(R * C) + 12.0 * double(R) + 8.0 * double(blocks * C));
+#define VC_XENT_BWD_COLSUM(NV)                                                                               \
+    launch(vec ? xent_backward_colsum_kernel<NV, true> : xent_backward_colsum_kernel<NV, false>,               \
+           dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, logits, targets, row_stats, grad_loss,           \
+           grad_loss_value, R, C, grad_logits, sums->part)
+        if (nv <= 1) VC_XENT_BWD_COLSUM(1);
+        else if (nv <= 2) VC_XENT_BWD_COLSUM(2);
+        else if (nv <= 4) VC_XENT_BWD_COLSUM(4);
+        else VC_XENT_BWD_COLSUM(8);
+#undef VC_XENT_BWD_COLSUM
+        after_launch("xent_backward");
+        p.done();
+    }
+    if (pending) *pending = sums.release();
+    else finish_colsum(*sums, column_sum);
+}
+
 }  // namespace
 }  // namespace vchip
 
@@ -806,22 +924,30 @@ extern "C" {
 
 int vc_hip_xent_forward(const float* logits, const int32_t* targets, size_t rows, size_t classes, float* row_stats,
                         float* loss) {
-    return guard([&] { xent_forward(logits, targets, rows, classes, row_stats, loss, nullptr); });
+    return guard([&] { xent_forward(logits, targets, rows, classes, row_stats, loss, nullptr, nullptr); });
 }
+
 
 int vc_hip_xent_forward_published(const float* logits, const int32_t* targets, size_t rows, size_t classes,
                                   float* row_stats, float* loss, vc_hip_mirror** mirror) {
     return guard([&] {
-        if (!mirror) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_xent_forward_published: null mirror");
-        require_device();
-        vc_hip_mirror* m = take_mirror();
-        try {
-            xent_forward(logits, targets, rows, classes, row_stats, loss, m);
-        } catch (...) {
-            give_mirror(m);
-            throw;
+        with_mirror(mirror, "vc_hip_xent_forward_published", [&](vc_hip_mirror* m) {
+            xent_forward(logits, targets, rows, classes, row_stats, loss, nullptr, m);
+        });
+    });
+}
+
+int vc_hip_xent_forward_argmax(const float* logits, const int32_t* targets, size_t rows, size_t classes,
+                               float* row_stats, float* loss, float* row_argmax, vc_hip_mirror** mirror) {
+    return guard([&] {
+        if (!row_argmax) fail(VC_HIP_ERR_INVALID_ARGUMENT, "vc_hip_xent_forward_argmax: null row_argmax");
+        if (!mirror) {
+            xent_forward(logits, targets, rows, classes, row_stats, loss, row_argmax, nullptr);
+            return;
         }
-        *mirror = m;
+        with_mirror(mirror, "vc_hip_xent_forward_argmax", [&](vc_hip_mirror* m) {
+            xent_forward(logits, targets, rows, classes, row_stats, loss, row_argmax, m);
+        });
     });
 }
 
@@ -842,42 +968,18 @@ int vc_hip_xent_backward_colsum(const float* logits, const int32_t* targets, con
                                 const float* grad_loss, float grad_loss_value, size_t rows, size_t classes,
                                 float* grad_logits, float* column_sum) {
     return guard([&] {
-        Device& d = require_device();
-        if (!column_sum) fail(VC_HIP_ERR_INVALID_ARGUMENT, "xent_backward_colsum: null column sum");
-        if (classes == 0) return;
-        if (classes > size_t(std::numeric_limits<int>::max())) fail(VC_HIP_ERR_OVERFLOW, "too many classes");
-        const int64_t R = int64_t(rows), C = int64_t(classes);
-        const int64_t nv = (C + kWave * 4 - 1) / (kWave * 4);
-        const bool fused = rows > 0 && nv <= 8;
-        const bool vec = C % 4 == 0 && aligned16(logits) && aligned16(grad_logits);
-        if (!fused) {  // the plain backward, then a separate reduction of dx
-            xent_backward(logits, targets, row_stats, grad_loss, grad_loss_value, rows, classes, grad_logits);
-            const int rc = vc_hip_reduce_axis(grad_logits, column_sum, 1, rows, classes, VC_REDUCE_SUM);
-            if (rc != VC_HIP_OK) fail(rc, std::string("column sum of the cross-entropy gradient: ") + vc_hip_last_error());
-            return;
-        }
-        const int64_t blocks = (R + kColRows - 1) / kColRows;
-        if (blocks > std::numeric_limits<int>::max()) fail(VC_HIP_ERR_OVERFLOW, "too many rows");
-        Scratch part(size_t(blocks) * size_t(C) * sizeof(double));
-        {
-            Profiled p("xent_backward", 0.0, 8.0 * double(R * C) + 12.0 * double(R) + 8.0 * double(blocks * C));
-#define VC_XENT_BWD_COLSUM(NV)                                                                               \
-    launch(vec ? xent_backward_colsum_kernel<NV, true> : xent_backward_colsum_kernel<NV, false>,               \
-           dim3(unsigned(blocks)), dim3(kBlock), 0, d.stream, logits, targets, row_stats, grad_loss,           \
-           grad_loss_value, R, C, grad_logits, part.as<double>())
-            if (nv <= 1) VC_XENT_BWD_COLSUM(1);
-            else if (nv <= 2) VC_XENT_BWD_COLSUM(2);
-            else if (nv <= 4) VC_XENT_BWD_COLSUM(4);
-            else VC_XENT_BWD_COLSUM(8);
-#undef VC_XENT_BWD_COLSUM
-            after_launch("xent_backward");
-            p.done();
-        }
-        Profiled pc("column_sum_combine", 0.0, 8.0 * double(blocks * C) + 4.0 * double(C));
-        launch(red::column_partials_kernel, dim3(unsigned((C + 63) / 64)), dim3(64 * red::kCombineWaves), 0, d.stream,
-               part.as<double>(), blocks, static_cast<const float*>(grad_logits), R, R, C, column_sum);
-        after_launch("column_sum_combine");
-        pc.done();
+        xent_backward_colsum(logits, targets, row_stats, grad_loss, grad_loss_value, rows, classes, grad_logits,
+                             column_sum, nullptr);
+    });
+}
+
+int vc_hip_xent_backward_colsum_pending(const float* logits, const int32_t* targets, const float* row_stats,
+                                        const float* grad_loss, float grad_loss_value, size_t rows, size_t classes,
+                                        float* grad_logits, float* column_sum, vc_hip_colsum** pending) {
+    return guard([&] {
+        if (!pending) fail(VC_HIP_ERR_INVALID_ARGUMENT, "xent_backward_colsum_pending: null handle pointer");
+        xent_backward_colsum(logits, targets, row_stats, grad_loss, grad_loss_value, rows, classes, grad_logits,
+                             column_sum, pending);
     });
 }
 

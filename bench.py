@@ -201,41 +201,84 @@ def _reference(cpu: bool):
     return K.Reference() if K.Reference.available() else None
 
 
-def measure_spiral(vc, W, ref):
-    """Spiral classifier train step (launch-bound; no roofline)."""
-    sp = W.spiral()
+def _small_mlp_step(vc, m):
+    """One train step of a one-hidden-layer classifier m (workloads.spiral or
+    workloads.mnist_shaped) on the hip device, ending with loss.item() as
+    benchmarks/train_benchmark.py:40-45 does."""
     ps = []
-    for w, b in zip(sp["weights"], sp["biases"]):
+    for w, b in zip(m["weights"], m["biases"]):
         ps += [vc.Tensor(w, requires_grad=True, device="hip"), vc.Tensor(b, requires_grad=True, device="hip")]
-    xs = vc.Tensor(sp["x"], device="hip")
+    xs = vc.Tensor(m["x"], device="hip")
+    targets = [int(t) for t in m["targets"]]
 
-    def spiral_step():
-        loss = vc.cross_entropy((xs @ ps[0] + ps[1]).relu() @ ps[2] + ps[3], sp["targets"])
+    def step():
+        loss = vc.cross_entropy((xs @ ps[0] + ps[1]).relu() @ ps[2] + ps[3], targets)
         loss.backward()
-        vc.sgd_step(ps, sp["lr"])
+        vc.sgd_step(ps, m["lr"])
         vc.zero_grad(ps)
         return loss.item()
 
+    return step
+
+
+def _small_mlp_figures(vc, step, warmup):
+    """Throughput over 200 steps drained at both ends (median of 5), and the
+    reference's own per-step measure: the median of 30 step times, each ending
+    with loss.item(), after 5 warm-up steps (benchmarks/train_benchmark.py:
+    71-79). loss.item() waits for the loss kernel only, so a step's host time
+    can end while its backward and update still run; the throughput figure
+    covers the device's whole work."""
     # Untimed warm-up long enough to reach the steady rate: the first few
     # hundred steps of a process run up to ~30% slower.
-    for _ in range(500):
-        spiral_step()
+    for _ in range(warmup):
+        step()
 
     def steps():
-        # Throughput over 200 steps with the device drained at both ends: loss.item()
-        # waits for the loss kernel only, so the host may run ahead of the device.
         vc.synchronize()
         for _ in range(200):
-            spiral_step()
+            step()
         vc.synchronize()
 
+    steps_per_s = 200e3 / _median_ms(steps, 5)
+    for _ in range(5):
+        step()
+    return {"hip_steps_per_s": round(steps_per_s, 1), "hip_median_step_ms": round(_median_ms(step, 30), 4)}
+
+
+def measure_spiral(vc, W, ref):
+    """Spiral classifier train step (launch-bound; no roofline)."""
+    sp = W.spiral()
     c1 = {"workload": "spiral 300x2->64->3 train step, lr 1.0", "bound": "launch/latency",
-          "hip_steps_per_s": round(200e3 / _median_ms(steps, 5), 1)}
+          **_small_mlp_figures(vc, _small_mlp_step(vc, sp), 500)}
     if ref:
         net = ref.mlp(sp["weights"], sp["biases"], sp["x"], sp["targets"])
         net.step(sp["lr"])
         c1["cpu_reference_steps_per_s"] = round(1e3 / _median_ms(lambda: net.step(sp["lr"]), 50), 1)
+    c1["published_reference_ms_per_step"] = {
+        "apple_m4_cpu": 0.749, "apple_m4_metal": 0.964,
+        "source": "docs/benchmarks.md:16-17 (benchmarks/train_benchmark.py, spiral_2-64-3_b300: the same shapes on "
+                  "N(0,1) inputs; Apple M4 under heavy load, per that file); context, not a target"}
     return c1
+
+
+def measure_mnist_shaped(vc, W, ref):
+    """The reference's MNIST-shaped train step, 256 x 784 -> 256 -> 10
+    (benchmarks/train_benchmark.py:23-26), with its own generator."""
+    mn = W.mnist_shaped()
+    out = {"workload": "MLP 784->256->10 fp32 (ReLU), batch 256: forward, softmax cross-entropy, backward, SGD lr 0.1",
+           "bound": "launch/latency", **_small_mlp_figures(vc, _small_mlp_step(vc, mn), 300)}
+    if ref:
+        net = ref.mlp(mn["weights"], mn["biases"], mn["x"], mn["targets"])
+        for _ in range(5):
+            net.step(mn["lr"])
+        ms = _median_ms(lambda: net.step(mn["lr"]), 30)
+        out["cpu_reference_median_step_ms"] = round(ms, 3)
+        out["cpu_reference_steps_per_s"] = round(1e3 / ms, 1)
+    out["published_reference_ms_per_step"] = {
+        "apple_m4_cpu": 6.346, "apple_m4_metal": 1.756,
+        "source": "docs/benchmarks.md:18-19 (benchmarks/train_benchmark.py, mnist_784-256-10_b256; Apple M4 under "
+                  "heavy load, per that file); context, not a target"}
+    return out
 
 
 def measure_bmm(vc, W, ref, bkey):
@@ -401,8 +444,9 @@ def measure_column_sums(vc):
     return out
 
 
-CONFIGS = ("spiral_train_step", "batched_matmul_backward", "batched_matmul_backward_broadcast_b",
-           "activation_backward", "cross_entropy", "column_sums", "mlp_one_hidden_layer")
+CONFIGS = ("spiral_train_step", "mnist_shaped_train_step", "batched_matmul_backward",
+           "batched_matmul_backward_broadcast_b", "activation_backward", "cross_entropy", "column_sums",
+           "mlp_one_hidden_layer")
 
 
 def config_measurements(cpu: bool, only=None):
@@ -414,6 +458,7 @@ def config_measurements(cpu: bool, only=None):
     ref = _reference(cpu)
     run = {
         "spiral_train_step": lambda: measure_spiral(vc, W, ref),
+        "mnist_shaped_train_step": lambda: measure_mnist_shaped(vc, W, ref),
         "batched_matmul_backward": lambda: measure_bmm(vc, W, ref, "b"),
         "batched_matmul_backward_broadcast_b": lambda: measure_bmm(vc, W, ref, "b_shared"),
         "activation_backward": lambda: measure_activation(vc, W, ref),

@@ -244,6 +244,33 @@ def test_mlp_workload_architecture_against_oracle(gemm_kernel):
         np.testing.assert_allclose(p.grad.numpy(), r.grad.data, rtol=1e-4, atol=1e-6)
 
 
+def test_mnist_shaped_steps_against_oracle(gemm_kernel):
+    """The reference's second train benchmark, 256 x 784 -> 256 -> 10 with its
+    own generator (benchmarks/train_benchmark.py:23-45): three steps of loss,
+    backward and SGD at lr 0.1 against the oracle's restatement."""
+    mn = W.mnist_shaped()
+    params = build_mlp(mn["weights"], mn["biases"])
+    x = H(mn["x"])
+    ref = A.Mlp(mn["weights"], mn["biases"])
+    xr = A.T(mn["x"])
+    targets = [int(t) for t in mn["targets"]]
+    for step in range(3):
+        loss = vc.cross_entropy(mlp_logits(params, x), targets)
+        loss.backward()
+        grads = [p.grad.numpy() for p in params]
+        vc.sgd_step(params, mn["lr"])
+        vc.zero_grad(params)
+        ref_loss = A.cross_entropy(ref.logits(xr), targets)
+        ref_loss.backward()
+        np.testing.assert_allclose(loss.item(), float(ref_loss.data), rtol=1e-5, err_msg=f"step {step}")
+        for g, r in zip(grads, ref.params()):
+            np.testing.assert_allclose(g, r.grad.data, rtol=1e-4, atol=1e-6, err_msg=f"step {step}")
+        A.sgd_step(ref.params(), mn["lr"])
+        A.zero_grad(ref.params())
+    for p, r in zip(params, ref.params()):
+        np.testing.assert_allclose(p.numpy(), r.data, rtol=1e-4, atol=1e-6)
+
+
 def mlp_backward_float64(m, zs):
     """Float64 gradients of mean cross-entropy through the ReLU MLP, evaluated
     on the given forward pre-activations zs (so the ReLU masks are the ones the

@@ -10,6 +10,8 @@ Workloads (seed in brackets):
   act      [2] y = sigmoid(relu(x + bias)) * exp(0.1 x), x [4096, 4096]
   xent     [3] softmax cross-entropy + argmax, logits [32768, 1000] ~ N(0, 2^2)
   mlp      [4] 8192 x 1024 -> 4096 -> 4096 -> 1000 MLP train step, SGD lr 0.01
+  mnist_shaped [0] 256 x 784 -> 256 -> 10 MLP train step, SGD lr 0.1 (the
+           reference's own train benchmark generator)
 """
 
 from __future__ import annotations
@@ -75,6 +77,23 @@ def mlp(batch=8192, dims=(1024, 4096, 4096, 1000), seed=4):
     targets = rng.integers(0, dims[-1], size=batch, dtype=np.int64)
     weights, biases = linear_weights(rng, list(dims))
     return dict(x=x, targets=targets, weights=weights, biases=biases, lr=0.01)
+
+
+def mnist_shaped(batch=256, features=784, hidden=256, classes=10, seed=0):
+    """The reference's second train benchmark (benchmarks/train_benchmark.py:
+    23-26, 29-45): x ~ N(0, 1) [batch, features], uniform int targets, then
+    each parameter drawn as N(0, 1) * scale in float64 and cast (W1 scale
+    features^-0.5, b1 0, W2 scale hidden^-0.5, b2 0), in that order; SGD lr 0.1."""
+    rng = np.random.default_rng(seed)
+    x = rng.normal(size=(batch, features)).astype(np.float32)
+    targets = rng.integers(0, classes, size=batch)
+
+    def param(shape, scale):
+        return (rng.normal(size=shape) * scale).astype(np.float32)
+
+    w1, b1 = param((features, hidden), features ** -0.5), param((hidden,), 0.0)
+    w2, b2 = param((hidden, classes), hidden ** -0.5), param((classes,), 0.0)
+    return dict(x=x, targets=targets.astype(np.int64), weights=[w1, w2], biases=[b1, b2], lr=0.1)
 
 
 def mlp_gemm_flops(batch, dims):

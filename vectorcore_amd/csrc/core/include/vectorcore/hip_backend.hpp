@@ -126,8 +126,11 @@ public:
     // first use; flush_elementwise computes every such storage of the scope
     // still referenced, those over the same elements in one program, and the
     // intermediate values nothing references any more are never written.
-    // Values are the same bits as the eager kernels'. On by default;
-    // VECTORCORE_HIP_FUSE=0 or set_fuse_elementwise(false) keeps every op eager.
+    // Elementwise values are the same bits as the eager kernels'. Column sums
+    // are added in a different fixed order from reduce_axis's: deterministic
+    // for either setting, they can differ in the last bit between the two. On
+    // by default; VECTORCORE_HIP_FUSE=0 or set_fuse_elementwise(false) keeps
+    // every op eager.
     class ElementwiseScope {
     public:
         ElementwiseScope();

@@ -15,15 +15,18 @@
 // with few tiles and a long K split K into ranges whose partial products are
 // summed in range order by a second pass.
 //
-// LDS holds both operand tiles k-contiguous, [128][32 + 4] floats, so a lane
-// reads 4 consecutive k with one ds_read_b128, feeding 4 MFMA steps (the +4
-// padding keeps those reads conflict-free). A k-contiguous operand (A in
-// NN/NT, B in NT/TT) is stored as loaded; an m/n-contiguous one (A in TN/TT,
-// B in NN/TN) is loaded as 4 x 4 blocks (4 k-rows of 4 m/n per thread) and
-// stored transposed.
-// Within each group of 8 k, half-wave 0 of a step takes k = 8g + s and
-// half-wave 1 takes k = 8g + 4 + s (s = 0..3): a fixed permutation of the
-// summation index applied identically to A and B.
+// Each operand tile sits in LDS as it is laid out in memory, so it is stored
+// as loaded. A k-contiguous operand (A in NN/NT, B in NT/TT) is [128][32 + 4]
+// floats: a lane reads 4 consecutive k with one ds_read_b128, feeding 4 MFMA
+// steps (the +4 padding keeps those reads conflict-free). An m/n-contiguous
+// operand (A in TN/TT, B in NN/TN) is [32][128]: a lane reads two adjacent
+// rows (columns) at one k with one ds_read_b64, feeding that step's MFMAs of
+// both 32-row blocks, so its blocks interleave (block b holds rows 2d + b of
+// the wave's 64). Within each group of 8 k, half-wave 0 of a step takes
+// k = 8g + s and half-wave 1 takes k = 8g + 4 + s (s = 0..3), in either
+// layout: a fixed permutation of the summation index applied identically to
+// A and B, so every C element adds its products in the same order whatever
+// the operands' layouts.
 //
 // Tile order: workgroups are dispatched round-robin over the 8 XCDs, each with
 // its own L2. Consecutive tile ids are remapped onto one XCD and walked in
@@ -46,7 +49,9 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 constexpr int BM = 128, BN = 128, BK = 32;
 constexpr int kThreads = 256;
 constexpr int kPadK = 4;                     // LDS row padding
-constexpr int kLdsTile = BM * (BK + kPadK);  // floats per operand tile: [128][32 + 4], k-contiguous
+constexpr int kLdsTile = BM * (BK + kPadK);  // floats per operand tile stage: [128][32 + 4] k-contiguous
+constexpr int kMnRow = BM;                   // an m/n-contiguous tile is [32][128] (fits in kLdsTile)
+static_assert(BK * kMnRow <= kLdsTile, "m/n-contiguous tile larger than a stage");
 constexpr int kGroupM = 8;
 #ifndef VC_NN_VIA_NT_MIN_ROWS
 #define VC_NN_VIA_NT_MIN_ROWS 4096
@@ -121,10 +126,10 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
 // Global -> register loader for one operand tile (128 along m/n, BK along k),
 // in four 16-byte slots per thread. Slot q of a k-contiguous operand is row
 // mn0 + 32 q, k k0..k0+3 (8 threads per 32-float row). Slot q of an
-// m/n-contiguous operand is k-row k0 + q, columns mn0..mn0+3: a thread's four
-// slots are a 4 x 4 block, and the 8 threads of one m/n range hold k 0..31, so
-// a load instruction reads 128-byte row segments and a transposed store
-// writes one whole LDS row per 8 lanes (no bank conflicts). Each thread keeps
+// m/n-contiguous operand is k-row k0 + 8 q, columns mn0..mn0+3 (32 threads
+// per 128-float row): a load instruction reads two whole 512-byte row
+// segments, and the LDS store of a slot writes one LDS row per 32 lanes (no
+// bank conflicts). Each thread keeps
 // one byte offset (slot 0); slots step by a uniform amount passed as the
 // instruction's scalar offset. The tile origin is uniform (scalar registers).
 // Edges are masked by pointing a slot out of range.
@@ -150,10 +155,10 @@ struct TileLoader {
             mn0 = t / (BK / 4);
             k0 = (t % (BK / 4)) * 4;
             qstep = 32u * ld4;
-        } else {  // eight threads cover one 128-byte row segment along m/n
-            k0 = (t % (BK / 4)) * 4;
-            mn0 = (t / (BK / 4)) * 4;
-            qstep = ld4;
+        } else {  // 32 threads cover one 128-float row along m/n
+            k0 = t / (BM / 4);
+            mn0 = (t % (BM / 4)) * 4;
+            qstep = 8u * ld4;
         }
         voff = KC ? uint32_t(mn0) * ld4 + uint32_t(k0) * 4u : uint32_t(k0) * ld4 + uint32_t(mn0) * 4u;
     }
@@ -162,7 +167,7 @@ struct TileLoader {
 
     // Slot q of slice kt. Slices past K read as zeros without touching memory.
     __device__ f4 load(__amdgpu_buffer_rsrc_t rs, int kt, int q) const {
-        const int k = kt * BK + k0 + (KC ? 0 : q);
+        const int k = kt * BK + k0 + (KC ? 0 : 8 * q);
         const int mn = mn0 + (KC ? 32 * q : 0);
         const uint32_t soff = uint32_t(q) * qstep;
         if (Vec) {
@@ -179,37 +184,54 @@ struct TileLoader {
         return v;
     }
 
-    // Byte offset in an LDS stage of this thread's first 16-byte store (row
-    // mn0, k k0); store q adds q * lds_qstep.
-    __device__ uint32_t lds_off() const { return uint32_t(mn0 * (BK + kPadK) + k0) * 4u; }
-    static constexpr uint32_t lds_qstep = KC ? 32u * (BK + kPadK) * 4u : uint32_t(BK + kPadK) * 4u;
+    // Byte offset in an LDS stage of this thread's first 16-byte store
+    // (m/n mn0, k k0); store q adds q * lds_qstep.
+    __device__ uint32_t lds_off() const {
+        return KC ? uint32_t(mn0 * (BK + kPadK) + k0) * 4u : uint32_t(k0 * kMnRow + mn0) * 4u;
+    }
+    static constexpr uint32_t lds_qstep = KC ? 32u * (BK + kPadK) * 4u : 8u * kMnRow * 4u;
 };
 
 // Store q (0..3) of this thread's slice registers into an LDS stage (`off`
-// from TileLoader::lds_off). Both operands sit k-contiguous in LDS: a
-// k-contiguous slot goes as it is; an m/n-contiguous operand's 4 x 4 block
-// goes transposed, store q being row mn0 + q = component q of the four slots.
+// from TileLoader::lds_off): every slot goes as loaded, in either layout.
 template <bool KC, bool Vec>
 __device__ inline void store_slot(char* __restrict__ lds, uint32_t off, const f4 (&v)[4], int q) {
-    f4 row;
-    if (KC) {
-        row = v[q];
-    } else {
-        row = f4{v[0][q], v[1][q], v[2][q], v[3][q]};
-    }
-    *reinterpret_cast<f4*>(lds + off + q * TileLoader<KC, Vec>::lds_qstep) = row;
+    *reinterpret_cast<f4*>(lds + off + q * TileLoader<KC, Vec>::lds_qstep) = v[q];
 }
 
-// Part s (0..3) of the fragments of k-group g for the wave's two 32-row
-// blocks at `off` and `off + 32`: frag[b][s'] is the value for MFMA step s'.
-// Block b's 4 values come with one ds_read_b128, at parts `first` and
-// `first + 1` (A uses parts 0-1, B parts 2-3, so each part issues one read).
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+// One operand's MFMA fragments of one k-group for the wave's two 32-row
+// blocks: at(b, s) is block b's value for MFMA step s. A k-contiguous tile
+// gives each block's 4 steps with one ds_read_b128; an m/n-contiguous tile
+// gives each step's 2 blocks (interleaved rows) with one ds_read_b64.
+template <bool KC>
+struct Frag;
+template <>
+struct Frag<true> {
+    f4 v[2];
+    __device__ float at(int b, int s) const { return v[b][s]; }
+};
+template <>
+struct Frag<false> {
+    f2 v[4];
+    __device__ float at(int b, int s) const { return v[s][b]; }
+};
+
+// Part s (0..3) of the fragments of k-group g for the wave's 64 rows at `off`.
+// A k-contiguous tile issues block b's read at part first + b (A uses parts
+// 0-1, B parts 2-3); an m/n-contiguous tile issues step s's read at part s.
+template <bool KC>
 __device__ inline void read_part(const float* __restrict__ lds, int off, int g, int lane, int s, int first,
-                                 f4 (&frag)[2]) {
-    const int r = off + (lane & 31);
+                                 Frag<KC>& frag) {
     const int kb = g * 8 + 4 * (lane >> 5);
-    const int b = s - first;
-    if (b == 0 || b == 1) frag[b] = *reinterpret_cast<const f4*>(lds + (r + 32 * b) * (BK + kPadK) + kb);
+    if constexpr (KC) {
+        const int b = s - first;
+        if (b == 0 || b == 1)
+            frag.v[b] = *reinterpret_cast<const f4*>(lds + (off + (lane & 31) + 32 * b) * (BK + kPadK) + kb);
+    } else {
+        frag.v[s] = *reinterpret_cast<const f2*>(lds + (kb + s) * kMnRow + off + 2 * (lane & 31));
+    }
 }
 
 // Vector-load variants fit two workgroups per CU (<= 256 VGPRs). The scalar-load
@@ -220,9 +242,8 @@ template <bool TA, bool TB, bool Vec>
 __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmArgs p) {
     // Two LDS stages. Step kt multiplies out of stage cur while its second
     // k-group also stores slice kt + 1 (in registers since step kt - 1) into
-    // the other stage and issues the global loads of slice kt + 2 (an
-    // m/n-contiguous operand in the third k-group, after its transposed stores
-    // have read all four slots). Storing in the second group rather than the
+    // the other stage and issues the global loads of slice kt + 2, each slot
+    // right after its store. Storing in the second group rather than the
     // first lets a tile's first step run a group of MFMAs while slice 1, loaded
     // just before it, is still arriving. Fragments are read one k-group ahead;
     // after the third group's MFMAs one barrier makes stage cur ^ 1 complete
@@ -296,11 +317,12 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
                 }
             }
             __syncthreads();
-            f4 fa[2][2], fb[2][2];  // [k-group parity][32-row block]
+            Frag<AKC> fa[2];  // [k-group parity]
+            Frag<BKC> fb[2];
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                read_part(As[0], wm, 0, lane, s, 0, fa[0]);
-                read_part(Bs[0], wn, 0, lane, s, 2, fb[0]);
+                read_part<AKC>(As[0], wm, 0, lane, s, 0, fa[0]);
+                read_part<BKC>(Bs[0], wn, 0, lane, s, 2, fb[0]);
             }
             for (int kt = kt_begin; kt < kt_end; ++kt) {
                 const int cur = (kt - kt_begin) & 1;
@@ -319,29 +341,28 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
                     if (g == BK / 8 - 1) __syncthreads();
 #pragma unroll
                     for (int s = 0; s < 4; ++s) {
-                        // Store q of the next stage at step q of k-group 1. A
-                        // k-contiguous operand then reloads slot q right away;
-                        // a transposed store reads all four slots, so that
-                        // operand reloads them in k-group 2.
+                        // Store q of the next stage at step q of k-group 1,
+                        // then reload slot q right away (a store reads its
+                        // own slot only, in either layout).
                         if (g == 1) {
                             store_slot<AKC, Vec>(st_a, a_st, ra, s);
                             store_slot<BKC, Vec>(st_b, b_st, rb, s);
+                            ra[s] = la.load(sa, kt + 2, s);
+                            rb[s] = lb.load(sb, kt + 2, s);
                         }
-                        if (g == (AKC ? 1 : 2)) ra[s] = la.load(sa, kt + 2, s);
-                        if (g == (BKC ? 1 : 2)) rb[s] = lb.load(sb, kt + 2, s);
                         if (g + 1 < BK / 8) {
-                            read_part(as, wm, g + 1, lane, s, 0, fa[cb ^ 1]);
-                            read_part(bs, wn, g + 1, lane, s, 2, fb[cb ^ 1]);
+                            read_part<AKC>(as, wm, g + 1, lane, s, 0, fa[cb ^ 1]);
+                            read_part<BKC>(bs, wn, g + 1, lane, s, 2, fb[cb ^ 1]);
                         } else {
-                            read_part(as_next, wm, 0, lane, s, 0, fa[cb ^ 1]);
-                            read_part(bs_next, wn, 0, lane, s, 2, fb[cb ^ 1]);
+                            read_part<AKC>(as_next, wm, 0, lane, s, 0, fa[cb ^ 1]);
+                            read_part<BKC>(bs_next, wn, 0, lane, s, 2, fb[cb ^ 1]);
                         }
 #pragma unroll
                         for (int i = 0; i < 2; ++i)
 #pragma unroll
                             for (int j = 0; j < 2; ++j)
-                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[cb][i][s], fb[cb][j][s], acc[i][j],
-                                                                                 0, 0, 0);
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[cb].at(i, s), fb[cb].at(j, s),
+                                                                                 acc[i][j], 0, 0, 0);
                         // Keep this order: the scheduler would otherwise sink
                         // each LDS read to just before its first use.
                         __builtin_amdgcn_sched_barrier(0);
@@ -362,17 +383,28 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
         const __amdgpu_buffer_rsrc_t rm =
             make_rsrc((masked ? p.relu_mask + z * int64_t(p.M) * p.N : C) + int64_t(m0) * p.N + n0);
         const int row_lim = p.M - m0, col_lim = p.N - n0;
-        const int row0 = wm + 4 * (lane >> 5);
+        // Tile coordinates of accumulator value v of block (i, j) on this
+        // lane (D row d = 8 (v / 4) + 4 (lane / 32) + v % 4, column lane % 32):
+        // a k-contiguous operand's blocks are 32 consecutive rows (columns),
+        // an m/n-contiguous one's interleave (block b holds 2 d + b).
+        // (The two forms below keep every variant within 256 registers: the
+        // register allocation of the masked epilogue, 64 mask loads in flight,
+        // follows how these indices are written.)
+        const int row0 = wm + 4 * (lane >> 5), col0 = wn + (lane & 31);
+        const auto crow = [&](int i, int v) {
+            return AKC ? row0 + 32 * i + 8 * (v >> 2) + (v & 3) : wm + 2 * (8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) + i;
+        };
+        const auto ccol = [&](int j) { return BKC ? col0 + 32 * j : wn + 2 * (lane & 31) + j; };
         if (masked) {  // all 64 mask loads in flight before the first use
             f16v x[2][2];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const int col = wn + 32 * j + (lane & 31);
+                    const int col = ccol(j);
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
-                        const int row = row0 + 32 * i + 8 * (v >> 2) + (v & 3);
+                        const int row = crow(i, v);
                         const bool ok = row < row_lim && col < col_lim;
                         x[i][j][v] = __builtin_bit_cast(
                             float, __builtin_amdgcn_raw_buffer_load_b32(
@@ -396,7 +428,7 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
                 const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.bias + n0);
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const int col = wn + 32 * j + (lane & 31);
+                    const int col = ccol(j);
                     bias[j] = __builtin_bit_cast(
                         float, __builtin_amdgcn_raw_buffer_load_b32(rb, col < col_lim ? uint32_t(col) * 4u : kOutOfRange,
                                                                     0, 0));
@@ -429,11 +461,11 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
                         const float value = acc[i][j][v];
-                        const int row = row0 + 32 * i + 8 * (v >> 2) + (v & 3);
+                        const int row = crow(i, v);
                         sum += whole || row < row_lim ? double(value) : 0.0;
                     }
                 sum += __shfl_xor(sum, 32, 64);
-                const int col = wn + 32 * j + (lane & 31);
+                const int col = ccol(j);
                 const uint64_t bits = __builtin_bit_cast(uint64_t, sum);
                 const uint32_t off = lane < 32 && col < col_lim ? uint32_t(col) * 8u : kOutOfRange;
                 __builtin_amdgcn_raw_buffer_store_b32(uint32_t(bits), rp, off, 0, 0);
@@ -444,10 +476,10 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int col = wn + 32 * j + (lane & 31);
+                const int col = ccol(j);
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const int row = row0 + 32 * i + 8 * (v >> 2) + (v & 3);
+                    const int row = crow(i, v);
                     const bool ok = row < row_lim && col < col_lim;
                     const float value = acc[i][j][v];  // element first: bit-casting the subscript takes lane 0
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), rc,

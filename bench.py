@@ -570,8 +570,9 @@ def main():
         "bwd_gemm_tflops": round(bwd_tflops, 2) if bwd_tflops else None,
         "fwd_gemm_tflops": round(fwd_tflops, 2) if fwd_tflops else None,
         "bias_grad_sums": {
-            "how": "column sums kept by the producing kernels (masked NT product epilogue for db1 and db2, "
-                   "cross-entropy backward for db3), then one fixed-order combine pass each",
+            "how": "partial column sums left pending by the producing kernels (masked NT product epilogue for "
+                   "db1 and db2, cross-entropy backward for db3) and finished inside the SGD launch; a separate "
+                   "combine launch would show here",
             "combine_launches_per_step": round(combine.get("launches", 0) / nb, 2),
             "combine_us_per_step": round(combine.get("ms", 0.0) * 1e3 / nb, 2),
         },

@@ -22,7 +22,6 @@ namespace {
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr unsigned kBlock = 256;
-constexpr int kWave = 64;
 
 __device__ inline f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 __device__ inline void st4(float* p, f4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p)); }
@@ -131,12 +130,17 @@ __global__ __launch_bounds__(kBlock) void map2_kernel(const float* __restrict__ 
 //
 // A tensor whose gradient is still a set of pending column sums (part[k]:
 // part_rows[k] partial rows of count[k] doubles, see red::combine_waves) has
-// no chunks; instead the first blocks of the grid finish those sums, 64
-// columns per block, and update the tensor with them: four waves stand in for
-// the 16 virtual waves of the fixed order (wave w takes w, w + 4, w + 8,
-// w + 12), so the gradient has the bits red::column_partials_kernel gives it.
-// These blocks come first so that their load round trips overlap the stream.
+// no chunks; instead the first blocks of the grid finish those sums, 16
+// columns per block, and update the tensor with them: thread t runs virtual
+// wave t / 16 of the fixed order for column t % 16 (eight loads in flight,
+// as red::column_partials_kernel's lanes do), and the 16 wave sums are added
+// in order, so the gradient has the bits red::column_partials_kernel gives it.
+// These blocks come first so that their load round trips overlap the stream;
+// keeping them to one virtual wave per thread keeps the kernel's registers,
+// and so the streaming blocks' occupancy, those of a plain update.
 constexpr int kAxpyList = 16;
+constexpr int kCombineCols = 16;
+static_assert(kBlock == kCombineCols * red::kCombineWaves, "one thread per (virtual wave, column)");
 struct AxpyList {
     float* o[kAxpyList];
     const float* t[kAxpyList];
@@ -150,32 +154,22 @@ struct AxpyList {
     float alpha;
 };
 
-constexpr int kCombineWavesPerBlock = kBlock / kWave;
-constexpr int kVirtualPerWave = red::kCombineWaves / kCombineWavesPerBlock;
-
 __global__ __launch_bounds__(kBlock) void axpy_list_kernel(AxpyList L) {
     const AxpyOp f{L.alpha};
     const int combine_blocks = L.combine_first[L.n];
     if (int(blockIdx.x) < combine_blocks) {
-        __shared__ double wave_sum[red::kCombineWaves][kWave];
+        __shared__ double wave_sum[red::kCombineWaves][kCombineCols];
         int k = 0;
         while (int(blockIdx.x) >= L.combine_first[k + 1]) ++k;
-        const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
-        const int64_t col = int64_t(int(blockIdx.x) - L.combine_first[k]) * kWave + lane;
-        double acc[kVirtualPerWave];
-        if (col < L.count[k]) {
-            red::combine_waves<kVirtualPerWave>(L.part[k], L.part_rows[k], L.count[k], col, w, kCombineWavesPerBlock,
-                                                acc);
-        } else {
-#pragma unroll
-            for (int i = 0; i < kVirtualPerWave; ++i) acc[i] = 0.0;
-        }
-#pragma unroll
-        for (int i = 0; i < kVirtualPerWave; ++i) wave_sum[w + i * kCombineWavesPerBlock][lane] = acc[i];
+        const int c = int(threadIdx.x) % kCombineCols, w = int(threadIdx.x) / kCombineCols;
+        const int64_t col = int64_t(int(blockIdx.x) - L.combine_first[k]) * kCombineCols + c;
+        double acc[1] = {0.0};
+        if (col < L.count[k]) red::combine_waves<1>(L.part[k], L.part_rows[k], L.count[k], col, w, 0, acc);
+        wave_sum[w][c] = acc[0];
         __syncthreads();
         if (w == 0 && col < L.count[k]) {
-            double total = wave_sum[0][lane];
-            for (int v = 1; v < red::kCombineWaves; ++v) total += wave_sum[v][lane];
+            double total = wave_sum[0][c];
+            for (int v = 1; v < red::kCombineWaves; ++v) total += wave_sum[v][c];
             L.o[k][col] = f(L.t[k][col], float(total));
         }
         return;
@@ -480,7 +474,7 @@ int vc_hip_axpy_batch_colsum(float* const* outputs, const float* const* targets,
                         fail(VC_HIP_ERR_INVALID_ARGUMENT, "axpy_batch: pending column sums of " +
                                                               std::to_string(pending->n) + " columns for a tensor of " +
                                                               std::to_string(counts[i]));
-                    const int64_t blocks = (pending->n + kWave - 1) / kWave;
+                    const int64_t blocks = (pending->n + kCombineCols - 1) / kCombineCols;
                     if (int64_t(L.combine_first[L.n]) + blocks > std::numeric_limits<int>::max() / 2)
                         fail(VC_HIP_ERR_OVERFLOW, "axpy_batch: too many pending columns");
                     L.part[L.n] = pending->part;

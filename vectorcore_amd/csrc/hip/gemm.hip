@@ -46,7 +46,11 @@ namespace {
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
+// (A 64-deep slice, with the 139 KB of two stages holding one workgroup per
+// CU, measured 2-7% slower on every product shape of the workloads.)
 constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int kSlots = BK / 8;                 // 16-byte global loads per thread per operand slice
+constexpr int kKcRowsPerSlot = 4 * 256 / BK;   // k-contiguous rows one slot of 256 threads covers
 constexpr int kThreads = 256;
 constexpr int kPadK = 4;                     // LDS row padding
 constexpr int kLdsTile = BM * (BK + kPadK);  // floats per operand tile stage: [128][32 + 4] k-contiguous
@@ -154,7 +158,7 @@ struct TileLoader {
         if (KC) {
             mn0 = t / (BK / 4);
             k0 = (t % (BK / 4)) * 4;
-            qstep = 32u * ld4;
+            qstep = uint32_t(kKcRowsPerSlot) * ld4;
         } else {  // 32 threads cover one 128-float row along m/n
             k0 = t / (BM / 4);
             mn0 = (t % (BM / 4)) * 4;
@@ -168,7 +172,7 @@ struct TileLoader {
     // Slot q of slice kt. Slices past K read as zeros without touching memory.
     __device__ f4 load(__amdgpu_buffer_rsrc_t rs, int kt, int q) const {
         const int k = kt * BK + k0 + (KC ? 0 : 8 * q);
-        const int mn = mn0 + (KC ? 32 * q : 0);
+        const int mn = mn0 + (KC ? kKcRowsPerSlot * q : 0);
         const uint32_t soff = uint32_t(q) * qstep;
         if (Vec) {
             const bool ok = mn < mn_lim && k < K;
@@ -189,13 +193,13 @@ struct TileLoader {
     __device__ uint32_t lds_off() const {
         return KC ? uint32_t(mn0 * (BK + kPadK) + k0) * 4u : uint32_t(k0 * kMnRow + mn0) * 4u;
     }
-    static constexpr uint32_t lds_qstep = KC ? 32u * (BK + kPadK) * 4u : 8u * kMnRow * 4u;
+    static constexpr uint32_t lds_qstep = KC ? uint32_t(kKcRowsPerSlot) * (BK + kPadK) * 4u : 8u * kMnRow * 4u;
 };
 
 // Store q (0..3) of this thread's slice registers into an LDS stage (`off`
 // from TileLoader::lds_off): every slot goes as loaded, in either layout.
 template <bool KC, bool Vec>
-__device__ inline void store_slot(char* __restrict__ lds, uint32_t off, const f4 (&v)[4], int q) {
+__device__ inline void store_slot(char* __restrict__ lds, uint32_t off, const f4 (&v)[kSlots], int q) {
     *reinterpret_cast<f4*>(lds + off + q * TileLoader<KC, Vec>::lds_qstep) = v[q];
 }
 
@@ -293,25 +297,25 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
             TileLoader<BKC, Vec> lb;
             la.init(p.a + aoff + r * p.a_rstride, p.lda, m0, p.M, p.K);
             lb.init(p.b + boff + r * p.b_rstride, p.ldb, n0, p.N, p.K);
-            f4 ra[4], rb[4];
+            f4 ra[kSlots], rb[kSlots];
             char* const lds_a = reinterpret_cast<char*>(As[0]);
             char* const lds_b = reinterpret_cast<char*>(Bs[0]);
             const uint32_t a_st = la.lds_off(), b_st = lb.lds_off();
             {
                 const __amdgpu_buffer_rsrc_t sa = la.slice(kt_begin), sb = lb.slice(kt_begin);
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < kSlots; ++q) {
                     ra[q] = la.load(sa, kt_begin, q);
                     rb[q] = lb.load(sb, kt_begin, q);
                 }
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < kSlots; ++q) {
                     store_slot<AKC, Vec>(lds_a, a_st, ra, q);
                     store_slot<BKC, Vec>(lds_b, b_st, rb, q);
                 }
                 const __amdgpu_buffer_rsrc_t na = la.slice(kt_begin + 1), nb = lb.slice(kt_begin + 1);
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < kSlots; ++q) {
                     ra[q] = la.load(na, kt_begin + 1, q);
                     rb[q] = lb.load(nb, kt_begin + 1, q);
                 }
@@ -344,11 +348,12 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
                         // Store q of the next stage at step q of k-group 1,
                         // then reload slot q right away (a store reads its
                         // own slot only, in either layout).
-                        if (g == 1) {
-                            store_slot<AKC, Vec>(st_a, a_st, ra, s);
-                            store_slot<BKC, Vec>(st_b, b_st, rb, s);
-                            ra[s] = la.load(sa, kt + 2, s);
-                            rb[s] = lb.load(sb, kt + 2, s);
+                        if (g >= 1 && g <= kSlots / 4) {
+                            const int q = 4 * (g - 1) + s;
+                            store_slot<AKC, Vec>(st_a, a_st, ra, q);
+                            store_slot<BKC, Vec>(st_b, b_st, rb, q);
+                            ra[q] = la.load(sa, kt + 2, q);
+                            rb[q] = lb.load(sb, kt + 2, q);
                         }
                         if (g + 1 < BK / 8) {
                             read_part<AKC>(as, wm, g + 1, lane, s, 0, fa[cb ^ 1]);

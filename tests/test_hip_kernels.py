@@ -469,9 +469,12 @@ def test_cross_entropy_matches_reference_fixture(golden):
 # Two rows per wavefront hold 1, 2, 4 or 8 float4s per lane (up to 128, 256,
 # 512, 1024 classes): 3, 37, 2 and 130 (scalar loads), 200 and 512 (vector
 # loads, 200 a partial last float4 slot), 257 and 1000; odd row counts leave
-# the last wavefront half a pair.
+# the last wavefront half a pair. One row per wavefront holds 8 or 16 float4s
+# per lane (up to 2048, 4096 classes); with the grid at the workgroups resident
+# at once (three or two per CU), 4000 x 1500 and 2100 x 4095 (scalar loads)
+# give waves more than one row.
 @pytest.mark.parametrize("rows,classes", [(512, 1000), (300, 3), (64, 37), (4, 2), (257, 200), (65, 130),
-                                          (33, 512), (31, 257)])
+                                          (33, 512), (31, 257), (4000, 1500), (2100, 4095)])
 def test_cross_entropy_against_oracle(rows, classes):
     from oracle import autograd as A
     xe = W.xent(rows=rows, classes=classes, seed=rows + classes)

@@ -510,10 +510,13 @@ __device__ inline void finish_loss(double* wave_terms, double* __restrict__ part
     }
 }
 
-// Rows of 1025 to 4096 classes. cur and next alone take 2 NV float4 per
-// lane (64 registers at NV 8, 128 at NV 16), so the allocation is left to the
-// compiler: any minimum of waves per SIMD (six, or four at NV 8 and two at
-// NV 16) made it spill to scratch.
+// Rows of 1025 to 4096 classes, one row per wavefront at a time. The row
+// takes NV float4 per lane (32 registers at NV 8, 64 at NV 16) and the
+// allocation is left to the compiler (132 and 229 registers: three and two
+// waves per SIMD; a minimum of waves per SIMD made it spill). The waves in
+// flight hide the loads: loading the next row while finishing this one took a
+// second register set, left three and one waves per SIMD, and measured 6% (2000
+// classes) and 26% (4096 classes) slower over 32768 rows.
 template <int NV, bool Vec>
 __global__ __launch_bounds__(kBlock) void xent_rows_cached_kernel(const float* __restrict__ x,
                                                                   const int* __restrict__ targets, int64_t rows,
@@ -526,27 +529,13 @@ __global__ __launch_bounds__(kBlock) void xent_rows_cached_kernel(const float* _
     const int64_t first = int64_t(blockIdx.x) * kRowsPerBlock + threadIdx.x / kWave;
     const int64_t waves = int64_t(gridDim.x) * kRowsPerBlock;
     double total = 0.0;  // lane 0: this wavefront's terms, in row order
-    if (first < rows) {
-        // The next row's target is loaded first and read after this row is
-        // finished, so waiting for it never waits for the row loads. (Two
-        // register sets taking turns instead of the copy below measured 5%
-        // slower: the duplicated row code needs more registers than 6 waves
-        // per SIMD leave.)
-        f4 cur[NV], next[NV];
-        load_row<Vec>(cur, x + first * len, len, lane);
-        int t = __builtin_amdgcn_readfirstlane(targets[first]);
-        for (int64_t r = first; r < rows; r += waves) {
-            const int64_t rn = r + waves;
-            int tn = 0;
-            if (rn < rows) {
-                tn = targets[rn];
-                load_row<Vec>(next, x + rn * len, len, lane);
-            }
-            total += double(finish_row<Vec>(cur, r, len, t, lane, stats, amax));
-#pragma unroll
-            for (int u = 0; u < NV; ++u) cur[u] = next[u];
-            t = __builtin_amdgcn_readfirstlane(tn);
-        }
+    // The target is loaded before the row, so waiting for it never waits for
+    // the row loads.
+    for (int64_t r = first; r < rows; r += waves) {
+        const int t = __builtin_amdgcn_readfirstlane(targets[r]);
+        f4 cur[NV];
+        load_row<Vec>(cur, x + r * len, len, lane);
+        total += double(finish_row<Vec>(cur, r, len, t, lane, stats, amax));
     }
     if (lane == 0) wave_terms[threadIdx.x / kWave] = total;
     finish_loss(wave_terms, part, rows, loss, host_loss);
@@ -776,6 +765,19 @@ void xent_backward(const float* logits, const int32_t* targets, const float* row
     p.done();
 }
 
+// Workgroups of xent_rows_cached_kernel<NV, Vec> resident on one CU at once
+// (its register use sets it; queried once per process).
+template <int NV, bool Vec>
+int64_t cached_resident_blocks() {
+    static const int64_t blocks = [] {
+        int b = 0;
+        const bool ok =
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, xent_rows_cached_kernel<NV, Vec>, kBlock, 0) == hipSuccess;
+        return ok && b > 0 ? int64_t(b) : int64_t(1);
+    }();
+    return blocks;
+}
+
 // The forward. With `publish`, the loss is also copied into that mirror's
 // host slot: by the finishing block of a register-held row kernel, whose
 // dispatch then carries the mirror's completion event, or, when the profiler
@@ -795,14 +797,25 @@ void xent_forward(const float* logits, const int32_t* targets, size_t rows, size
     Profiled p("xent_forward", 0.0,
                4.0 * double(R * C) + 4.0 * double(R) + 8.0 * double(R) + (row_argmax ? 4.0 * double(R) : 0.0));
     // Rows are held in registers: up to 1024 classes two rows per wavefront,
-    // up to 4096 one row per wavefront (NV float4 per lane); at most 8
-    // workgroups per CU walk the rows (3 to 12 per CU measured within 3%).
-    // Longer rows are streamed.
+    // up to 4096 one row per wavefront (NV float4 per lane). At most 8
+    // workgroups per CU walk the two-row kernel's rows (3 to 12 per CU
+    // measured within 3%); the one-row kernel takes as many as are resident
+    // at once (two or three per CU), so no workgroup waits for a CU to free up
+    // (8 per CU measured 5-40% slower). Longer rows are streamed.
     const int64_t nv = (C + kWave * 4 - 1) / (kWave * 4);
-    const unsigned cached_grid = unsigned(std::min<int64_t>(
-        {(R + kRowsPerBlock - 1) / kRowsPerBlock, int64_t(d.cu_count) * kXentBlocksPerCu,
-         int64_t(red::kMaxFinishBlocks)}));
-    Scratch part(size_t(std::max<int64_t>(cached_grid, (R + red::sum_chunk(R) - 1) / red::sum_chunk(R))) *
+    const int64_t nh = (C + 127) / 128;  // float4s per lane with a half-wave per row
+    int64_t row_blocks = 0;              // grid of the register-held row kernel
+    if (nh <= 8) {
+        row_blocks = std::min<int64_t>({(R + 2 * kRowsPerBlock - 1) / (2 * kRowsPerBlock),
+                                        int64_t(d.cu_count) * kXentBlocksPerCu, int64_t(red::kMaxFinishBlocks)});
+    } else if (nv <= 16) {
+        const int64_t resident = nv <= 8 ? (vec ? cached_resident_blocks<8, true>() : cached_resident_blocks<8, false>())
+                                         : (vec ? cached_resident_blocks<16, true>() : cached_resident_blocks<16, false>());
+        row_blocks = std::min<int64_t>({(R + kRowsPerBlock - 1) / kRowsPerBlock,
+                                        int64_t(d.cu_count) * std::min(kXentBlocksPerCu, resident),
+                                        int64_t(red::kMaxFinishBlocks)});
+    }
+    Scratch part(size_t(std::max<int64_t>(row_blocks, (R + red::sum_chunk(R) - 1) / red::sum_chunk(R))) *
                  sizeof(double));
     // Register-held rows (nv <= 16) write the loss's host copy from their
     // finishing block, the dispatch signalling the mirror, unless the
@@ -821,13 +834,10 @@ void xent_forward(const float* logits, const int32_t* targets, size_t rows, size
             launch(kernel, dim3(blocks), dim3(kBlock), 0, d.stream, logits, targets, R, C, row_stats, row_argmax,
                    part.as<double>(), loss, host_loss);
     };
-    const int64_t nh = (C + 127) / 128;  // float4s per lane with a half-wave per row
     if (nh <= 8) {
         // Rows of at most 1024 classes: two per wavefront.
-        const unsigned half_grid = unsigned(std::min<int64_t>(
-            {(R + 2 * kRowsPerBlock - 1) / (2 * kRowsPerBlock), int64_t(d.cu_count) * kXentBlocksPerCu,
-             int64_t(red::kMaxFinishBlocks)}));
-#define VC_XENT_HALF(NV) row_launch(vec ? xent_half_rows_kernel<NV, true> : xent_half_rows_kernel<NV, false>, half_grid)
+#define VC_XENT_HALF(NV) \
+    row_launch(vec ? xent_half_rows_kernel<NV, true> : xent_half_rows_kernel<NV, false>, unsigned(row_blocks))
         if (nh <= 1) VC_XENT_HALF(1);
         else if (nh <= 2) VC_XENT_HALF(2);
         else if (nh <= 4) VC_XENT_HALF(4);
@@ -846,7 +856,7 @@ void xent_forward(const float* logits, const int32_t* targets, size_t rows, size
         // Register-held rows; the row kernel sums the terms per block and
         // its last block finishes the loss.
 #define VC_XENT_ROWS(NV) \
-    row_launch(vec ? xent_rows_cached_kernel<NV, true> : xent_rows_cached_kernel<NV, false>, cached_grid)
+    row_launch(vec ? xent_rows_cached_kernel<NV, true> : xent_rows_cached_kernel<NV, false>, unsigned(row_blocks))
         if (nv <= 8) VC_XENT_ROWS(8);  // rows of more than 1024 classes: nv >= 5
         else VC_XENT_ROWS(16);
 #undef VC_XENT_ROWS

@@ -56,15 +56,20 @@ def test_gemm_matches_reference_fixture(golden, gemm_kernel, m, k, n):
                                        err_msg=f"trans_a={ta} trans_b={tb}")
 
 
-# The first nine shapes are above the small-product threshold (2^20
-# multiply-adds with K <= 1024), so with "mfma" they run on the MFMA kernel:
-# a whole tile, a partial K slice (60, 129), partial m and n tiles (130, 70,
-# 257, 383), and vector and scalar loads in all four transposes. The last
-# three run on the FMA kernel with either setting: K in one slice (7), and
-# K over two and four of its 256-deep slices (300, 1000), the last partial.
+# The first nine shapes are above the FMA kernel's threshold (2^20
+# multiply-adds with K <= 1024), so with "mfma" they run on a matrix-core
+# kernel: the 32 x 32 tiles of small products up to (512, 1024, 1000), the
+# 128 x 128 tiles from 65 of them (1030, 129, 1100) and (1100, 256, 1030), and
+# (1, 4096, 3) with K split across 128 x 128 workgroups. Covered: a whole
+# tile, a partial K slice (60, 129), partial m and n tiles (130, 70, 257, 383,
+# 1030, 1100), and vector and scalar loads in all four transposes. The last
+# three run on the FMA kernel with either setting, except that "mfma" gives
+# (64, 300, 3) with A transposed (a weight gradient, K the batch) to the
+# 32 x 32 tiles: K in one slice (7), and K over two and four of its 256-deep
+# slices (300, 1000), the last partial.
 @pytest.mark.parametrize("m,k,n", [(256, 64, 128), (192, 256, 64), (256, 60, 128), (130, 64, 128), (256, 64, 70),
-                                   (257, 129, 383), (512, 1024, 1000), (1, 4096, 3), (2000, 7, 129), (1000, 7, 1),
-                                   (64, 300, 3), (2, 1000, 64)])
+                                   (257, 129, 383), (512, 1024, 1000), (1030, 129, 1100), (1100, 256, 1030),
+                                   (1, 4096, 3), (2000, 7, 129), (1000, 7, 1), (64, 300, 3), (2, 1000, 64)])
 def test_gemm_edges_against_oracle(gemm_kernel, m, k, n):
     rng = np.random.default_rng(m * 7 + k * 3 + n)
     for ta in (0, 1):
@@ -75,9 +80,32 @@ def test_gemm_edges_against_oracle(gemm_kernel, m, k, n):
                                        rtol=1e-4, atol=1e-4 * np.sqrt(k), err_msg=f"trans_a={ta} trans_b={tb}")
 
 
-def test_gemm_batched_offsets_affine_and_table(gemm_kernel):
+# Products on both sides of the rule that gives small products the 32 x 32
+# tiles (gemm_small_kernel: up to 64 tiles of 128 x 128 with K <= 2048, or 9 to
+# 32 tiles with any K) and the rest the 128 x 128 tiles (K split across
+# workgroups when they are few): checked against float64 with the reference's
+# tolerance and repeated bit for bit.
+@pytest.mark.parametrize("m,k,n,batch", [(1024, 1024, 1024, 1), (1100, 2100, 300, 1), (300, 4100, 1100, 1),
+                                         (65, 2047, 4033, 1), (100, 515, 90, 5), (1100, 2100, 500, 1),
+                                         (2049, 1024, 1025, 1), (96, 4100, 96, 2), (40, 8192, 40, 1)])
+def test_gemm_on_both_sides_of_the_small_tile_rule(m, k, n, batch):
+    rng = np.random.default_rng(m + 3 * k + 7 * n + batch)
+    for ta, tb in ((0, 0), (1, 0), (0, 1), (1, 1)):
+        a = rng.uniform(-1, 1, size=(batch,) + ((k, m) if ta else (m, k))).astype(np.float32)
+        b = rng.uniform(-1, 1, size=(batch,) + ((n, k) if tb else (k, n))).astype(np.float32)
+        got = run_gemm(a, b, m, k, n, ta, tb, batch=batch)
+        want = np.matmul((a.transpose(0, 2, 1) if ta else a).astype(np.float64),
+                         (b.transpose(0, 2, 1) if tb else b).astype(np.float64))
+        np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4 * np.sqrt(k),
+                                   err_msg=f"{m}x{k}x{n} b{batch} ta={ta} tb={tb}")
+        np.testing.assert_array_equal(run_gemm(a, b, m, k, n, ta, tb, batch=batch), got)
+
+
+@pytest.mark.parametrize("m,k,n", [(33, 70, 41), (200, 300, 150)])
+def test_gemm_batched_offsets_affine_and_table(gemm_kernel, m, k, n):
+    # (33, 70, 41) runs on the FMA kernel, (200, 300, 150) with "mfma" on the
+    # 32 x 32 tiles.
     rng = np.random.default_rng(3)
-    m, k, n = 33, 70, 41
     a = rng.standard_normal((4, m, k)).astype(np.float32)
     b = rng.standard_normal((2, k, n)).astype(np.float32)
     # batch z reads a[z] and b[z % 2]: not affine, goes through the offset table

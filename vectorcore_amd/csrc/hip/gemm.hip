@@ -13,7 +13,9 @@
 // the device). K advances in slices of 32 through two LDS stages with one
 // barrier per slice (the pipeline is described at gemm_mfma_kernel). Outputs
 // with few tiles and a long K split K into ranges whose partial products are
-// summed in range order by a second pass.
+// summed in range order by a second pass. Products of a few dozen such tiles
+// at most run on 32 x 32 tiles instead, K split over a workgroup's four waves
+// (gemm_small_kernel), and tiny ones on the FMA kernel (gemm_simple_kernel).
 //
 // Each operand tile sits in LDS as it is laid out in memory, so it is stored
 // as loaded. A k-contiguous operand (A in NN/NT, B in NT/TT) is [128][32 + 4]
@@ -35,6 +37,7 @@
 #include "vc_hip_internal.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <limits>
 #include <optional>
 #include <string>
@@ -678,9 +681,131 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
     }
 }
 
+// Small products (a few 128 x 128 tiles, K too long for the FMA kernel): a
+// 256-thread workgroup computes one 32 x 32 tile of C as one
+// V_MFMA_F32_32X32X2_F32 block per wave, wave w taking the 32-deep K chunks
+// w, w + 4, ..., and the four partial tiles are added in wave order through
+// LDS, so one launch finishes the product in a fixed order. Operands go from
+// memory straight into the MFMA operand layout, no LDS staging: in chunk c,
+// half-wave h of MFMA step j takes k = 32 c + 16 h + j (a fixed permutation of
+// the summation index, identical for A and B), lane l row (A) or column (B)
+// l % 32. A k-contiguous operand is read as four 16-byte loads per lane and
+// chunk (vec), an m/n-contiguous one as 16 loads of 32 consecutive floats per
+// half-wave. The next chunk's loads are issued before this chunk's MFMAs.
+// col_part: one partial row per 32-row tile.
+constexpr int kSmallTile = 32;
+// Element `elem` of a buffer (4 floats from it: small_ld4), or 0 when !ok.
+__device__ inline float small_ld1(__amdgpu_buffer_rsrc_t rs, uint32_t elem, bool ok) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? elem * 4u : kOutOfRange, 0, 0));
+}
+__device__ inline f4 small_ld4(__amdgpu_buffer_rsrc_t rs, uint32_t elem, bool ok) {
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? elem * 4u : kOutOfRange, 0, 0));
+}
+
+template <bool TA, bool TB, bool Vec>
+struct SmallChunk {
+    float a[16], b[16];
+    // The 16 k from k0 of A (row `row` of op(A)) and B (column `col` of
+    // op(B)); elements outside op(A) / op(B) read as 0.
+    __device__ void load(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, const GemmArgs& p, int row, int col,
+                         int k0) {
+        const bool row_ok = row < p.M, col_ok = col < p.N;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int k = k0 + 4 * q;
+            if constexpr (!TA && Vec) {  // A [M][K]: 16 consecutive k of one row
+                const f4 v = small_ld4(ra, uint32_t(row * p.lda + k), row_ok && k < p.K);
+                a[4 * q] = v.x, a[4 * q + 1] = v.y, a[4 * q + 2] = v.z, a[4 * q + 3] = v.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    a[4 * q + e] = small_ld1(ra, TA ? uint32_t((k + e) * p.lda + row) : uint32_t(row * p.lda + k + e),
+                                             row_ok && k + e < p.K);
+            }
+            if constexpr (TB && Vec) {  // B [N][K]: 16 consecutive k of one column
+                const f4 v = small_ld4(rb, uint32_t(col * p.ldb + k), col_ok && k < p.K);
+                b[4 * q] = v.x, b[4 * q + 1] = v.y, b[4 * q + 2] = v.z, b[4 * q + 3] = v.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    b[4 * q + e] = small_ld1(rb, TB ? uint32_t(col * p.ldb + k + e) : uint32_t((k + e) * p.ldb + col),
+                                             col_ok && k + e < p.K);
+            }
+        }
+    }
+};
+
+template <bool TA, bool TB, bool Vec>
+__global__ __launch_bounds__(kThreads) void gemm_small_kernel(GemmArgs p) {
+    __shared__ float part[4][16][64];                   // [wave][accumulator v][lane]
+    __shared__ float tile[kSmallTile][kSmallTile + 1];  // final values, for the column sums
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tm = int(blockIdx.x) / p.tiles_n, tn = int(blockIdx.x) % p.tiles_n;
+    const int m0 = tm * kSmallTile, n0 = tn * kSmallTile;
+    const int half = lane >> 5;
+    const int chunks = (p.K + 31) / 32;
+    for (int64_t z = blockIdx.y; z < p.batch; z += gridDim.y) {
+        const int64_t aoff = uniform64(p.table ? p.table[2 * z] : z * p.a_bstride);
+        const int64_t boff = uniform64(p.table ? p.table[2 * z + 1] : z * p.b_bstride);
+        f16v acc;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+        for (int64_t r = 0; r < p.reduce; ++r) {
+            const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + aoff + r * p.a_rstride);
+            const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b + boff + r * p.b_rstride);
+            const int row = m0 + (lane & 31), col = n0 + (lane & 31);
+            SmallChunk<TA, TB, Vec> cur, next;
+            if (wave < chunks) cur.load(ra, rb, p, row, col, 32 * wave + 16 * half);
+            for (int c = wave; c < chunks; c += 4) {
+                if (c + 4 < chunks) next.load(ra, rb, p, row, col, 32 * (c + 4) + 16 * half);
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[j], cur.b[j], acc, 0, 0, 0);
+                cur = next;
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) part[wave][v][lane] = acc[v];
+        __syncthreads();
+        // Thread t finishes accumulator slots (v, l) = t / 64 + 4 i, t % 64:
+        // the four waves' partials in wave order, then the epilogue.
+        float* C = p.c + z * int64_t(p.M) * p.N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int v = int(threadIdx.x) / 64 + 4 * i, l = int(threadIdx.x) % 64;
+            float value = part[0][v][l];
+            value += part[1][v][l];
+            value += part[2][v][l];
+            value += part[3][v][l];
+            const int tr = 8 * (v / 4) + 4 * (l / 32) + v % 4, tc = l % 32;  // the MFMA's D layout
+            const int row = m0 + tr, col = n0 + tc;
+            const bool inside = row < p.M && col < p.N;
+            const int64_t t = int64_t(row) * p.N + col;
+            if (inside) {
+                if (p.relu_mask) value = value * (p.relu_mask[z * int64_t(p.M) * p.N + t] > 0.0f ? 1.0f : 0.0f);
+                if (p.bias || p.relu) value = bias_relu(value, p.bias ? p.bias[col] : 0.0f, p.relu != 0);
+                C[t] = value;
+            }
+            tile[tr][tc] = inside ? value : 0.0f;
+        }
+        if (p.col_part) {  // batch 1: the tile's 32 rows of each column, in row order, in double
+            __syncthreads();
+            if (threadIdx.x < kSmallTile && n0 + int(threadIdx.x) < p.N) {
+                double sum = 0.0;
+                for (int rr = 0; rr < kSmallTile; ++rr) sum += double(tile[rr][threadIdx.x]);
+                p.col_part[int64_t(tm) * p.N + n0 + threadIdx.x] = sum;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 template <bool TA, bool TB>
-void launch_variant(const GemmArgs& args, bool vec, bool simple, dim3 grid, hipStream_t stream) {
-    if (simple) {
+void launch_variant(const GemmArgs& args, bool vec, bool simple, bool small, dim3 grid, hipStream_t stream) {
+    if (small) {
+        if (vec) launch((gemm_small_kernel<TA, TB, true>), grid, dim3(kThreads), 0, stream, args);
+        else launch((gemm_small_kernel<TA, TB, false>), grid, dim3(kThreads), 0, stream, args);
+    } else if (simple) {
         if (args.K <= 16) launch((gemm_simple_kernel<TA, TB, 16>), grid, dim3(256), 0, stream, args);
         else if (args.K <= 64) launch((gemm_simple_kernel<TA, TB, 64>), grid, dim3(256), 0, stream, args);
         else launch((gemm_simple_kernel<TA, TB, 256>), grid, dim3(256), 0, stream, args);
@@ -693,6 +818,23 @@ void launch_variant(const GemmArgs& args, bool vec, bool simple, dim3 grid, hipS
 
 const char* variant_label(bool ta, bool tb) {
     return ta ? (tb ? "gemm_tt" : "gemm_tn") : (tb ? "gemm_nt" : "gemm_nn");
+}
+
+// Whether a product takes gemm_small_kernel rather than the 128 x 128 tiles
+// (tiles128 of them, times `products` matrices) or the FMA kernel (tiny).
+// Measured on MI355X: the 32 x 32 tiles run at up to ~60 TFLOP/s, while 9 to
+// 64 tiles of 128 x 128 leave most CUs idle (1024^3: 37.8 against 68.2 us;
+// 512 x 8192 x 512: 86 against 145 us). Up to 8 tiles and K above 2048, the
+// larger tiles split K 32 ways and win (256 x 4096 x 256: 27 against 42 us);
+// from 128 tiles they are as fast or faster (2048 x 1024^2: 69 against 72 us;
+// 2048^2 x 1024: 80 against 133 us). Among tiny products, weight gradients
+// (A transposed, K the batch, at least 128) gain from the four waves' K split
+// (256 x 300 x 64: 6.1 against 12.1 us); the others stay on the FMA kernel.
+bool small_tiles(int64_t K, int64_t products, int64_t tiles128, bool tiny, bool ta, bool tb) {
+    if (tiny) return ta && !tb && K >= 128;
+    const int64_t work = tiles128 * products;
+    if (work <= 64 && K <= 2048) return true;
+    return work > 8 && work <= 32;
 }
 
 // offsets: nullptr for the affine mode (a_bstride / b_bstride).
@@ -734,9 +876,16 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     // a 128 x 128 MFMA tile there is mostly padding, and its fixed latency
     // (~8 us, plus a second pass when K is split) is several times the FMA
     // kernel's whole run (one memory round trip per 256 k).
-    const bool simple = force_simple || (double(M) * double(N) * double(K) * double(batch) * double(reduce) <=
-                                             kTinyMacs && K <= kSimpleMaxK);
-    const int64_t tiles = simple ? tiles_m_simple * tiles_n_simple : tiles_m * tiles_n;
+    const bool tiny = double(M) * double(N) * double(K) * double(batch) * double(reduce) <= kTinyMacs &&
+                      K <= kSimpleMaxK;
+    const int64_t tiles_m32 = (M + kSmallTile - 1) / kSmallTile, tiles_n32 = (N + kSmallTile - 1) / kSmallTile;
+    // A product of a few 128 x 128 tiles takes 32 x 32 tiles with K split over
+    // the workgroup's four waves (gemm_small_kernel): one launch, no split pass.
+    // Its operand offsets are 32-bit from the operand's origin.
+    const bool small_fits = M * K < (int64_t(1) << 29) && K * N < (int64_t(1) << 29) && M * N < (int64_t(1) << 29);
+    const bool small = !force_simple && small_fits && small_tiles(K, batch * reduce, tiles_m * tiles_n, tiny, ta, tb);
+    const bool simple = !small && (force_simple || tiny);
+    const int64_t tiles = small ? tiles_m32 * tiles_n32 : simple ? tiles_m_simple * tiles_n_simple : tiles_m * tiles_n;
     if (tiles > std::numeric_limits<int>::max() / 2) fail(VC_HIP_ERR_OVERFLOW, "matmul output has too many tiles");
     // Byte offsets relative to a tile origin are 32-bit: 128 rows of any
     // operand or of C must span less than 2 GiB.
@@ -760,8 +909,8 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     args.reduce = reduce;
     args.a_rstride = a_rstride;
     args.b_rstride = b_rstride;
-    args.tiles_m = int(simple ? tiles_m_simple : tiles_m);
-    args.tiles_n = int(simple ? tiles_n_simple : tiles_n);
+    args.tiles_m = int(small ? tiles_m32 : simple ? tiles_m_simple : tiles_m);
+    args.tiles_n = int(small ? tiles_n32 : simple ? tiles_n_simple : tiles_n);
 
     // 16-byte vector loads need every row start and batch offset on a 4-float boundary.
     bool vec = aligned16(a) && aligned16(b) && args.lda % 4 == 0 && args.ldb % 4 == 0 && a_rstride % 4 == 0 &&
@@ -785,7 +934,7 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     int splits = 1;
     int64_t r_per_split = reduce;
     const int64_t want = (2 * int64_t(d.cu_count) + tiles * batch - 1) / (tiles * batch);
-    if (!simple && tiles * batch < 2 * int64_t(d.cu_count)) {
+    if (!simple && !small && tiles * batch < 2 * int64_t(d.cu_count)) {
         if (reduce > 1) {
             r_per_split = (reduce + std::min(want, reduce) - 1) / std::min(want, reduce);
             splits = int((reduce + r_per_split - 1) / r_per_split);
@@ -818,17 +967,17 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     // adds them next, or they are handed to the caller as pending sums. A
     // split product's C is summed again afterwards instead.
     ColsumPtr sums;
-    if (column_sum && splits == 1) sums = new_colsum(simple ? tiles_m_simple : 2 * tiles_m, N);
+    if (column_sum && splits == 1) sums = new_colsum(small ? tiles_m32 : simple ? tiles_m_simple : 2 * tiles_m, N);
     if (sums) args.col_part = sums->part;
     const double bytes =
         4.0 * (double(M * K + K * N) * double(reduce) + double(M * N) * (relu_mask ? 2.0 : 1.0)) * double(batch) +
         (bias ? 4.0 * double(N) : 0.0);
     std::optional<Profiled> prof;
     if (!in_caller_scope) prof.emplace(label, flops, bytes);
-    if (ta && tb) launch_variant<true, true>(args, vec, simple, grid, d.stream);
-    else if (ta) launch_variant<true, false>(args, vec, simple, grid, d.stream);
-    else if (tb) launch_variant<false, true>(args, vec, simple, grid, d.stream);
-    else launch_variant<false, false>(args, vec, simple, grid, d.stream);
+    if (ta && tb) launch_variant<true, true>(args, vec, simple, small, grid, d.stream);
+    else if (ta) launch_variant<true, false>(args, vec, simple, small, grid, d.stream);
+    else if (tb) launch_variant<false, true>(args, vec, simple, small, grid, d.stream);
+    else launch_variant<false, false>(args, vec, simple, small, grid, d.stream);
     if (splits > 1) {
         after_launch(label);
         const int64_t total = batch * M * N;

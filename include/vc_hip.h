@@ -64,9 +64,10 @@ const char* vc_hip_device_name(void);
 /* MetalBackend::last_error (metal_backend.hpp:20): thread-local message of
  * the last failing call on this thread, or why the device is unavailable. */
 const char* vc_hip_last_error(void);
-/* MetalBackend::gemm_kernel (metal_backend.hpp:22): "mfma" (MFMA tiles),
- * "simple" (portable FMA tiles, forced by VECTORCORE_HIP_GEMM=simple),
- * or "unavailable". */
+/* MetalBackend::gemm_kernel (metal_backend.hpp:22): "mfma" (matrix-core
+ * tiles: 128 x 128, or 32 x 32 for products of a few tiles, and the FMA
+ * tiles for tiny products), "simple" (portable FMA tiles for every product,
+ * forced by VECTORCORE_HIP_GEMM=simple), or "unavailable". */
 const char* vc_hip_gemm_kernel(void);
 /* Selects the GEMM kernel for later calls: "mfma" or "simple". The reference
  * picks its kernel once, from VECTORCORE_METAL_GEMM=tiled

@@ -757,11 +757,12 @@ __global__ __launch_bounds__(kThreads) void gemm_small_kernel(GemmArgs p) {
             SmallChunk<TA, TB, Vec> cur, next;
             if (wave < chunks) cur.load(ra, rb, p, row, col, 32 * wave + 16 * half);
             for (int c = wave; c < chunks; c += 4) {
-                if (c + 4 < chunks) next.load(ra, rb, p, row, col, 32 * (c + 4) + 16 * half);
+                const bool more = c + 4 < chunks;
+                if (more) next.load(ra, rb, p, row, col, 32 * (c + 4) + 16 * half);
 #pragma unroll
                 for (int j = 0; j < 16; ++j)
                     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[j], cur.b[j], acc, 0, 0, 0);
-                cur = next;
+                if (more) cur = next;
             }
         }
 #pragma unroll

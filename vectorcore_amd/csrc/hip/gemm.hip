@@ -14,7 +14,7 @@
 // barrier per slice (the pipeline is described at gemm_mfma_kernel). Outputs
 // with few tiles and a long K split K into ranges whose partial products are
 // summed in range order by a second pass. Products of a few dozen such tiles
-// at most run on 32 x 32 tiles instead, K split over a workgroup's four waves
+// at most run on 32 x 32 tiles instead, K split over a workgroup's eight waves
 // (gemm_small_kernel), and tiny ones on the FMA kernel (gemm_simple_kernel).
 //
 // Each operand tile sits in LDS as it is laid out in memory, so it is stored
@@ -682,9 +682,9 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(GemmArgs p) {
 }
 
 // Small products (a few 128 x 128 tiles, K too long for the FMA kernel): a
-// 256-thread workgroup computes one 32 x 32 tile of C as one
+// workgroup of W = kSmallWaves waves computes one 32 x 32 tile of C as one
 // V_MFMA_F32_32X32X2_F32 block per wave, wave w taking the 32-deep K chunks
-// w, w + 4, ..., and the four partial tiles are added in wave order through
+// w, w + W, ..., and the W partial tiles are added in wave order through
 // LDS, so one launch finishes the product in a fixed order. Operands go from
 // memory straight into the MFMA operand layout, no LDS staging: in chunk c,
 // half-wave h of MFMA step j takes k = 32 c + 16 h + j (a fixed permutation of
@@ -735,9 +735,15 @@ struct SmallChunk {
     }
 };
 
+// Eight waves measured 5-18% faster than four on the products this kernel
+// takes (1024^3: 38.1 against 42.5 us; 512 x 8192 x 512: 62.5 against 75.8);
+// sixteen spill registers.
+constexpr int kSmallWaves = 8;  // waves (K shares) per 32 x 32 tile
+constexpr int kSmallThreads = 64 * kSmallWaves;
+
 template <bool TA, bool TB, bool Vec>
-__global__ __launch_bounds__(kThreads) void gemm_small_kernel(GemmArgs p) {
-    __shared__ float part[4][16][64];                   // [wave][accumulator v][lane]
+__global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(GemmArgs p) {
+    __shared__ float part[kSmallWaves][16][64];         // [wave][accumulator v][lane]
     __shared__ float tile[kSmallTile][kSmallTile + 1];  // final values, for the column sums
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int tm = int(blockIdx.x) / p.tiles_n, tn = int(blockIdx.x) % p.tiles_n;
@@ -756,9 +762,9 @@ __global__ __launch_bounds__(kThreads) void gemm_small_kernel(GemmArgs p) {
             const int row = m0 + (lane & 31), col = n0 + (lane & 31);
             SmallChunk<TA, TB, Vec> cur, next;
             if (wave < chunks) cur.load(ra, rb, p, row, col, 32 * wave + 16 * half);
-            for (int c = wave; c < chunks; c += 4) {
-                const bool more = c + 4 < chunks;
-                if (more) next.load(ra, rb, p, row, col, 32 * (c + 4) + 16 * half);
+            for (int c = wave; c < chunks; c += kSmallWaves) {
+                const bool more = c + kSmallWaves < chunks;
+                if (more) next.load(ra, rb, p, row, col, 32 * (c + kSmallWaves) + 16 * half);
 #pragma unroll
                 for (int j = 0; j < 16; ++j)
                     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[j], cur.b[j], acc, 0, 0, 0);
@@ -768,16 +774,15 @@ __global__ __launch_bounds__(kThreads) void gemm_small_kernel(GemmArgs p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) part[wave][v][lane] = acc[v];
         __syncthreads();
-        // Thread t finishes accumulator slots (v, l) = t / 64 + 4 i, t % 64:
-        // the four waves' partials in wave order, then the epilogue.
+        // Thread t finishes accumulator slots (v, l) = t / 64 + W i, t % 64
+        // (W waves): the waves' partials in wave order, then the epilogue.
         float* C = p.c + z * int64_t(p.M) * p.N;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int v = int(threadIdx.x) / 64 + 4 * i, l = int(threadIdx.x) % 64;
+        for (int i = 0; i < 16 / kSmallWaves; ++i) {
+            const int v = int(threadIdx.x) / 64 + kSmallWaves * i, l = int(threadIdx.x) % 64;
             float value = part[0][v][l];
-            value += part[1][v][l];
-            value += part[2][v][l];
-            value += part[3][v][l];
+#pragma unroll
+            for (int w = 1; w < kSmallWaves; ++w) value += part[w][v][l];
             const int tr = 8 * (v / 4) + 4 * (l / 32) + v % 4, tc = l % 32;  // the MFMA's D layout
             const int row = m0 + tr, col = n0 + tc;
             const bool inside = row < p.M && col < p.N;
@@ -804,8 +809,8 @@ __global__ __launch_bounds__(kThreads) void gemm_small_kernel(GemmArgs p) {
 template <bool TA, bool TB>
 void launch_variant(const GemmArgs& args, bool vec, bool simple, bool small, dim3 grid, hipStream_t stream) {
     if (small) {
-        if (vec) launch((gemm_small_kernel<TA, TB, true>), grid, dim3(kThreads), 0, stream, args);
-        else launch((gemm_small_kernel<TA, TB, false>), grid, dim3(kThreads), 0, stream, args);
+        if (vec) launch((gemm_small_kernel<TA, TB, true>), grid, dim3(kSmallThreads), 0, stream, args);
+        else launch((gemm_small_kernel<TA, TB, false>), grid, dim3(kSmallThreads), 0, stream, args);
     } else if (simple) {
         if (args.K <= 16) launch((gemm_simple_kernel<TA, TB, 16>), grid, dim3(256), 0, stream, args);
         else if (args.K <= 64) launch((gemm_simple_kernel<TA, TB, 64>), grid, dim3(256), 0, stream, args);
@@ -823,13 +828,14 @@ const char* variant_label(bool ta, bool tb) {
 
 // Whether a product takes gemm_small_kernel rather than the 128 x 128 tiles
 // (tiles128 of them, times `products` matrices) or the FMA kernel (tiny).
-// Measured on MI355X: the 32 x 32 tiles run at up to ~60 TFLOP/s, while 9 to
-// 64 tiles of 128 x 128 leave most CUs idle (1024^3: 37.8 against 68.2 us;
+// Measured on MI355X with four waves per 32 x 32 tile (eight are faster
+// still): the 32 x 32 tiles run at up to ~60 TFLOP/s, while 9 to 64 tiles of
+// 128 x 128 leave most CUs idle (1024^3: 37.8 against 68.2 us;
 // 512 x 8192 x 512: 86 against 145 us). Up to 8 tiles and K above 2048, the
 // larger tiles split K 32 ways and win (256 x 4096 x 256: 27 against 42 us);
 // from 128 tiles they are as fast or faster (2048 x 1024^2: 69 against 72 us;
 // 2048^2 x 1024: 80 against 133 us). Among tiny products, weight gradients
-// (A transposed, K the batch, at least 128) gain from the four waves' K split
+// (A transposed, K the batch, at least 128) gain from the waves' K split
 // (256 x 300 x 64: 6.1 against 12.1 us); the others stay on the FMA kernel.
 bool small_tiles(int64_t K, int64_t products, int64_t tiles128, bool tiny, bool ta, bool tb) {
     if (tiny) return ta && !tb && K >= 128;
@@ -881,7 +887,7 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
                       K <= kSimpleMaxK;
     const int64_t tiles_m32 = (M + kSmallTile - 1) / kSmallTile, tiles_n32 = (N + kSmallTile - 1) / kSmallTile;
     // A product of a few 128 x 128 tiles takes 32 x 32 tiles with K split over
-    // the workgroup's four waves (gemm_small_kernel): one launch, no split pass.
+    // the workgroup's eight waves (gemm_small_kernel): one launch, no split pass.
     // Its operand offsets are 32-bit from the operand's origin.
     const bool small_fits = M * K < (int64_t(1) << 29) && K * N < (int64_t(1) << 29) && M * N < (int64_t(1) << 29);
     const bool small = !force_simple && small_fits && small_tiles(K, batch * reduce, tiles_m * tiles_n, tiny, ta, tb);

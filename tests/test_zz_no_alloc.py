@@ -35,6 +35,7 @@ PAIRS = [
     ((1, 5000, 300, C.ARGMAX), (1, 900, 70, C.ARGMAX)),  # a long axis split into segments
     ((1, 5000, 300, C.MAX), (2, 400, 33, C.MAX)),
     ((4096, 1000, 1, C.ARGMAX), (100, 37, 1, C.SUM)),    # rows: no partial results
+    ((2, 100, 131000, C.SUM), (1, 70, 500, C.SUM)),      # one segment per column: sums written directly, no partials
 ]
 
 

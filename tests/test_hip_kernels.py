@@ -83,11 +83,14 @@ def test_gemm_edges_against_oracle(gemm_kernel, m, k, n):
 # Products on both sides of the rule that gives small products the 32 x 32
 # tiles (gemm_small_kernel: up to 64 tiles of 128 x 128 with K <= 2048, or 9 to
 # 32 tiles with any K) and the rest the 128 x 128 tiles (K split across
-# workgroups when they are few): checked against float64 with the reference's
+# workgroups when they are few: 1100 x 2100 x 500 in two ranges of at least 32
+# slices; 2000 x 1100 x 700 (96 tiles) and two 700 x 1500 x 1200 (120 tiles) in
+# two ranges of at least 16): checked against float64 with the reference's
 # tolerance and repeated bit for bit.
 @pytest.mark.parametrize("m,k,n,batch", [(1024, 1024, 1024, 1), (1100, 2100, 300, 1), (300, 4100, 1100, 1),
                                          (65, 2047, 4033, 1), (100, 515, 90, 5), (1100, 2100, 500, 1),
-                                         (2049, 1024, 1025, 1), (96, 4100, 96, 2), (40, 8192, 40, 1)])
+                                         (2049, 1024, 1025, 1), (96, 4100, 96, 2), (40, 8192, 40, 1),
+                                         (2000, 1100, 700, 1), (700, 1500, 1200, 2)])
 def test_gemm_on_both_sides_of_the_small_tile_rule(m, k, n, batch):
     rng = np.random.default_rng(m + 3 * k + 7 * n + batch)
     for ta, tb in ((0, 0), (1, 0), (0, 1), (1, 1)):

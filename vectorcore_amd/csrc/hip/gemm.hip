@@ -933,7 +933,7 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     }
     // Split the work when the output has fewer tiles than two workgroups per
     // CU: a batch reduction (reduce > 1) splits into ranges of r, a long K into
-    // ranges of at least 32 slices (at most 4), and the K of a tiny output
+    // ranges of at least 32 slices (16 for 65 to 128 tiles; at most 4 ranges), and the K of a tiny output
     // (<= kTinyTiles tiles) into up to 32 ranges. Each split accumulates into
     // its own partial matrix and a second pass sums the partials in split
     // order (deterministic). No split range is empty.
@@ -952,6 +952,13 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
         } else if (kt_total >= 64) {
             splits = int(std::min<int64_t>(want, 4));
             splits = std::min(splits, kt_total / 32);
+        } else if (4 * tiles * batch <= 2 * int64_t(d.cu_count) && kt_total >= 32) {
+            // 65 to 128 tiles (fewer take the 32 x 32 tiles) with K of 1024
+            // to 2047 fill at most a quarter of the workgroup slots: ranges of
+            // at least 16 slices fill them (2048 x 1024 x 1024: 72 -> 50 us;
+            // splitting 256 tiles this way measured slower, 81 -> 90 us).
+            splits = int(std::min<int64_t>(want, 4));
+            splits = std::min(splits, kt_total / 16);
         }
     }
     if (reduce == 1 && splits > 1)  // drop the ranges that ceil(kt_total / splits) slices each would leave empty

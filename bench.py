@@ -177,6 +177,20 @@ def _median_ms(fn, reps):
     return statistics.median(times)
 
 
+# Untimed calls before a configuration's timed ones. The part raises its
+# clock over the first tens of milliseconds of sustained load (batched matmul
+# backward: 0.69 of peak on its first calls, 0.83 after 50 more, 25 ms), so
+# each configuration first runs its call for this long, as a training loop
+# would have before.
+CONFIG_WARM_S = 0.1
+
+
+def _warm_up(fn, seconds=CONFIG_WARM_S):
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        fn()
+
+
 def _profiled(vc, fn, labels=None, repeats=5, setup=None):
     """Per-label kernel aggregates of one call of fn (events on the kernels'
     dispatches), averaged over `repeats` calls; `setup` runs untimed before each."""
@@ -294,7 +308,7 @@ def measure_bmm(vc, W, ref, bkey):
         vc.zero_grad([a, b])
         vc.synchronize()
 
-    fwd_bwd()
+    _warm_up(fwd_bwd)
     prof = _profiled(vc, fwd_bwd, labels=list(BWD_GEMM_LABELS))
     ms = sum(v["ms"] for v in prof.values())
     tflops = 2 * flops / ms / 1e9
@@ -324,7 +338,10 @@ def measure_activation(vc, W, ref):
         holder["y"].backward(dy)
         vc.synchronize()
 
-    forward(); backward(); vc.zero_grad([x, bias])
+    def fwd_bwd():
+        forward(); backward(); vc.zero_grad([x, bias])
+
+    _warm_up(fwd_bwd)
 
     def fresh_forward():
         vc.zero_grad([x, bias])
@@ -335,10 +352,6 @@ def measure_activation(vc, W, ref):
     kms = sum(v["ms"] for v in prof.values())
     kbytes = sum(v["bytes"] for v in prof.values())
     min_bytes = 3 * 4096 * 4096 * 4 + 2 * 4096 * 4
-
-    def fwd_bwd3():
-        forward(); backward(); vc.zero_grad([x, bias])
-
     c3 = {"workload": "x [4096,4096] + bias [1,4096]: sigmoid(relu) * exp(0.1 x), backward dx and dbias",
           "bound": "hbm", "bwd_kernel_gbs": round(kbytes / kms / 1e6, 1),
           "frac": round(kbytes / kms / 1e6 / HBM_PEAK_GBS, 3), "bwd_kernels_ms": round(kms, 3),
@@ -346,7 +359,7 @@ def measure_activation(vc, W, ref):
           "bwd_bytes_mb": round(kbytes / 1e6, 1),
           "min_bytes_rate_gbs": round(min_bytes / kms / 1e6, 1),
           "per_label_us": {k: round(v["ms"] * 1e3, 1) for k, v in prof.items()},
-          "hip_ms_forward_backward": round(_median_ms(fwd_bwd3, 10), 3)}
+          "hip_ms_forward_backward": round(_median_ms(fwd_bwd, 10), 3)}
     if ref:
         c3["cpu_reference_ms_forward_backward"] = round(
             _median_ms(lambda: ref.activation_backward(ac["x"], ac["bias"], ac["dy"]), 1), 1)
@@ -366,7 +379,7 @@ def measure_xent(vc, W, ref):
         vc.zero_grad([lg])
         vc.synchronize()
 
-    ce()
+    _warm_up(ce)
     prof = _profiled(vc, ce)
     c4 = {"workload": "logits [32768,1000] N(0,4): loss, dlogits, argmax(1)", "bound": "hbm",
           "hip_ms": round(_median_ms(ce, 10), 3)}
@@ -387,12 +400,11 @@ ONE_HIDDEN_STEPS = 20
 def measure_mlp_one_hidden(vc, W, ref):
     """The one-hidden-layer network 8192 x 1024 -> 4096 -> 1000 (the headline
     runs 1024 -> 4096 -> 4096 -> 1000): the same train step, seed and
-    initialisation; steps/s over ONE_HIDDEN_STEPS steps after 3 warm-up steps,
+    initialisation; steps/s over ONE_HIDDEN_STEPS steps after CONFIG_WARM_S of untimed steps,
     and the backward GEMMs' rate from events on their dispatches."""
     m = W.mlp(batch=BATCH, dims=ONE_HIDDEN_DIMS)
     step = mlp_step(vc, m)
-    for _ in range(3):
-        step()
+    _warm_up(step)
     vc.synchronize()
     vc.hip_profile(True, labels=list(BWD_GEMM_LABELS))
     vc.hip_profile_reset()
@@ -433,7 +445,12 @@ def measure_column_sums(vc):
     total_bytes = total_ms = 0.0
     for rows, cols, times in ((BATCH, 4096, 2), (BATCH, 1000, 1)):
         t = vc.Tensor(rng.standard_normal((rows, cols)).astype(np.float32), device="hip")
-        t.sum(0)
+
+        def colsum():
+            t.sum(0)
+            vc.synchronize()
+
+        _warm_up(colsum)
         prof = _profiled(vc, lambda: t.sum(0), labels=["reduce_axis_sum"], repeats=10)["reduce_axis_sum"]
         gbs = prof["bytes"] / prof["ms"] / 1e6
         out[f"{rows}x{cols}"] = {"us": round(prof["ms"] * 1e3, 2), "gbs": round(gbs, 1),

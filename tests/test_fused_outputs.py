@@ -165,11 +165,15 @@ def _masked_product(m, k, n, seed):
     return a, b, mask
 
 
-# MFMA tiles (whole, a partial last tile, a last tile of fewer than 64 rows),
-# the FMA kernel (small products; 300 rows leave a partial 16-row tile), and a
-# product split along K (no partial rows: the sums are written at once).
-PENDING_SHAPES = [(1024, 256, 512, "mfma"), (1000, 128, 300, "mfma"), (130, 64, 257, "mfma"), (300, 3, 64, "mfma"),
-                  (37, 16, 70, "mfma"), (700, 96, 200, "simple"), (64, 8192, 256, "mfma")]
+# 128 x 128 MFMA tiles (72 and 81 of them: a partial last tile of 104 rows,
+# a last tile of 6 rows, fewer than one wave's 64), 32 x 32 MFMA tiles (a few
+# 128 x 128 tiles' worth: whole, a partial last tile of 8 rows, of 2 rows),
+# the FMA kernel (tiny products, and forced; 300 rows leave a partial 16-row
+# tile), and a product split along K (no partial rows: the sums are written
+# at once).
+PENDING_SHAPES = [(1000, 128, 1100, "mfma"), (1030, 64, 1100, "mfma"), (1024, 256, 512, "mfma"),
+                  (1000, 128, 300, "mfma"), (130, 64, 257, "mfma"), (300, 3, 64, "mfma"), (37, 16, 70, "mfma"),
+                  (700, 96, 200, "simple"), (64, 8192, 256, "mfma")]
 
 
 @pytest.mark.parametrize("m,k,n,kernel", PENDING_SHAPES)
@@ -203,13 +207,14 @@ def test_pending_product_sums_finish_to_the_column_sum_entry_points_bits(m, k, n
     np.testing.assert_allclose(s1.numpy(), want, rtol=1e-6, atol=1e-6 * np.abs(c).sum(0).max())
 
 
-def test_pending_sums_leave_out_rows_past_the_matrix_even_when_b_is_infinite():
+@pytest.mark.parametrize("m,n", [(200, 128), (1030, 1100)])  # 32 x 32 tiles; 128 x 128 tiles, 6 rows in the last
+def test_pending_sums_leave_out_rows_past_the_matrix_even_when_b_is_infinite(m, n):
     # In a last, partial MFMA tile the rows past M hold 0 * B; with an
     # infinite entry of B that is NaN, which must not reach the sums. Here
     # every real row of column 5 is +inf (a positive A entry times the +inf
     # of B, unmasked), so its sum is +inf, and NaN would mean padding rows
     # were added.
-    m, k, n = 200, 64, 128
+    k = 64
     a, b, mask = _masked_product(m, k, n, 3)
     a[:, 7] = np.abs(a[:, 7]) + 0.5
     b[5, 7] = np.inf

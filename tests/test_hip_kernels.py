@@ -159,14 +159,16 @@ def test_gemm_relu_mask_is_gemm_then_relu_backward_bitexact(gemm_kernel):
 
 
 @pytest.mark.parametrize("m,k,n", [(300, 257, 130), (128, 64, 200), (100, 70, 33), (4096, 512, 1000),
-                                   (2048, 4096, 64), (8192, 1000, 4096)])
+                                   (1000, 256, 1100), (1030, 128, 1030), (2048, 4096, 64), (8192, 1000, 4096)])
 def test_masked_product_with_column_sums(gemm_kernel, m, k, n):
     """vc_hip_matmul_relu_mask_colsum: the product is vc_hip_matmul_relu_mask's
     bits, and the column sums equal the reduction of that product (the
     oracle's sequential double sum) to the last bit or within 1e-6. Covers
-    full and partial 128-row tiles, one tile, no full tile, a split-K shape
-    (2048 x 4096 x 64: the sums come from a separate reduction) and the
-    portable kernel (the same)."""
+    128 x 128 tiles (whole rows; a partial last tile of 104 rows; one of 6
+    rows), 32 x 32 tiles (a few 128 x 128 tiles' worth: 300 x 130, 128 x
+    200), the FMA kernel (100 x 33), a split-K shape (2048 x 4096 x 64: the
+    sums come from a separate reduction) and the portable kernel (the
+    same)."""
     rng = np.random.default_rng(m + k + n)
     a = rng.uniform(-1, 1, size=(m, k)).astype(np.float32)
     b = rng.uniform(-1, 1, size=(n, k)).astype(np.float32)
@@ -185,11 +187,14 @@ def test_masked_product_with_column_sums(gemm_kernel, m, k, n):
     assert (got == want).mean() > 0.99
 
 
-def test_column_sums_leave_out_rows_past_the_matrix():
+# 32 x 32 tiles (6 full tiles of rows, then 8 rows); 128 x 128 tiles (7 full
+# tiles of rows, then 104 rows)
+@pytest.mark.parametrize("m,n", [(200, 96), (1000, 1100)])
+def test_column_sums_leave_out_rows_past_the_matrix(m, n):
     # An infinity in B makes the padded rows of the last tile NaN (0 * inf);
     # those rows are not part of C and must not reach the sums.
     rng = np.random.default_rng(5)
-    m, k, n = 200, 64, 96  # one full tile of rows, then 72 rows of a partial tile
+    k = 64
     a = rng.uniform(0.5, 1, size=(m, k)).astype(np.float32)
     b = rng.uniform(-1, 1, size=(n, k)).astype(np.float32)
     b[7, 3] = np.inf

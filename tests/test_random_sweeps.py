@@ -1,10 +1,11 @@
 """Seeded random sweeps of C-ABI entry points against the oracle.
 
 GEMM (the four entry points): shapes mix tile edges (1..513 around the
-128-wide tiles), odd sizes, long K over few tiles (split K), misaligned
-operands (the element-load variants), batches with affine, broadcast and
-permuted per-batch offsets, batch reductions, the folded ReLU mask (zeros and
-NaN in the mask) and the bias + ReLU epilogue. Bar: the reference's GEMM
+128-wide tiles), odd sizes, long K over few tiles (split K), and two more
+sweeps cover the ranges of products that run on 32 x 32 and on 128 x 128
+tiles; misaligned operands (the element-load variants), batches with affine,
+broadcast and permuted per-batch offsets, batch reductions, the folded ReLU
+mask (zeros and NaN in the mask) and the bias + ReLU epilogue. Bar: the reference's GEMM
 tolerance, rtol 1e-4 and atol 1e-4 sqrt(k)
 (tests/python/test_performance_paths.py:43).
 
@@ -25,6 +26,7 @@ pytestmark = pytest.mark.gpu
 
 EDGE = [1, 2, 3, 4, 5, 7, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257, 383, 511, 513]
 CASES = 160
+LARGE_CASES = 60  # about 1 G multiply-adds each for the oracle
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -54,11 +56,58 @@ def _oracle(a_h, a_off, b_h, b_off, m, k, n, ta, tb):
     return K.matmul2d(a, b, bool(ta), bool(tb))
 
 
-def _case(rng, index):
-    kind = ["matmul", "matmul", "mask", "bias", "reduce"][index % 5]
+def _shape(rng):
     m, n, k = _dim(rng, 600), _dim(rng, 600), _dim(rng, 1500)
     if rng.random() < 0.15:  # a long K over a few output tiles: K is split
         m, n, k = int(rng.integers(1, 200)), int(rng.integers(1, 200)), int(rng.integers(2000, 6000))
+    return m, n, k
+
+
+SMALL_EDGE = [1, 2, 3, 31, 32, 33, 63, 64, 65, 95, 96, 97, 127, 128, 129, 255, 256, 257]
+K_EDGE = [1, 2, 15, 16, 17, 31, 32, 33, 255, 256, 257, 511, 512, 513, 2047, 2048]
+
+
+def _small_shape(rng):
+    """Shapes of at most 16 output tiles of 128 x 128 (times up to 3 batches
+    or 4 reduced products) and K up to 2048, the range that runs on 32 x 32
+    tiles with K split over a workgroup's waves: edges of the 32-row tiles,
+    K around the 16-wide half-wave steps and the 256-wide rounds of 8 waves,
+    and 9 to 25 tiles with K from 2049 to 4000 (no split pass)."""
+    if rng.random() < 0.15:
+        return int(rng.integers(257, 641)), int(rng.integers(257, 641)), int(rng.integers(2049, 4001))
+
+    def dim(edges, high):
+        return int(rng.choice(edges)) if rng.random() < 0.45 else int(rng.integers(1, high))
+
+    m, n = dim(SMALL_EDGE, 513), dim(SMALL_EDGE, 513)
+    return m, n, dim(K_EDGE, 2049)
+
+
+LARGE_EDGE = [895, 896, 897, 1023, 1024, 1025, 1151, 1152, 1153, 1279, 1280, 1281, 1407, 1408]
+
+
+def _large_shape(rng):
+    """Shapes of about 64 to 121 output tiles of 128 x 128, the range that
+    runs on those tiles: edges of the 128-row tiles (8 x 8 = 64 tiles is the
+    last product on 32 x 32 tiles), K 1024 to 2048 over up to 128 tiles (K
+    split in 2 to 4 ranges of at least 16 slices), and 25 to 64 tiles with K
+    from 2049 to 4000 (split when over 32 tiles)."""
+    r = rng.random()
+    if r < 0.25:
+        return int(rng.integers(1025, 1409)), int(rng.integers(897, 1409)), int(rng.integers(1024, 2049))
+    if r < 0.4:
+        return int(rng.integers(513, 1025)), int(rng.integers(513, 1025)), int(rng.integers(2049, 4001))
+
+    def dim():
+        return int(rng.choice(LARGE_EDGE)) if rng.random() < 0.45 else int(rng.integers(897, 1409))
+
+    m, n = dim(), dim()
+    return m, n, _dim(rng, 1200)
+
+
+def _case(rng, index, shape=_shape):
+    kind = ["matmul", "matmul", "mask", "bias", "reduce"][index % 5]
+    m, n, k = shape(rng)
     ta, tb = int(rng.integers(0, 2)), int(rng.integers(0, 2))
     shift = int(rng.choice([0, 0, 0, 1, 2]))  # elements of misalignment of both operands
     label = f"case {index}: {kind} m={m} k={k} n={n} trans=({ta},{tb}) shift={shift}"
@@ -116,6 +165,20 @@ def test_gemm_entry_points_random_sweep():
     rng = np.random.default_rng(20261201)
     for index in range(CASES):
         label, got, want, k = _case(rng, index)
+        np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4 * np.sqrt(k), err_msg=label)
+
+
+def test_gemm_entry_points_random_sweep_over_the_32_tile_range():
+    rng = np.random.default_rng(20261203)
+    for index in range(CASES):
+        label, got, want, k = _case(rng, index, _small_shape)
+        np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4 * np.sqrt(k), err_msg=label)
+
+
+def test_gemm_entry_points_random_sweep_over_the_128_tile_range():
+    rng = np.random.default_rng(20261204)
+    for index in range(LARGE_CASES):
+        label, got, want, k = _case(rng, index, _large_shape)
         np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4 * np.sqrt(k), err_msg=label)
 
 

@@ -65,11 +65,17 @@ const char* vc_hip_device_name(void);
  * the last failing call on this thread, or why the device is unavailable. */
 const char* vc_hip_last_error(void);
 /* MetalBackend::gemm_kernel (metal_backend.hpp:22): "mfma" (matrix-core
- * tiles: 128 x 128, or 32 x 32 for products of a few tiles, and the FMA
- * tiles for tiny products), "simple" (portable FMA tiles for every product,
- * forced by VECTORCORE_HIP_GEMM=simple), or "unavailable". */
+ * tiles by shape: 256 x 256 for large products, 128 x 128, or 32 x 32 for
+ * products of a few tiles, and the FMA tiles for tiny products), "simple"
+ * (portable FMA tiles for every product, forced by VECTORCORE_HIP_GEMM=simple),
+ * "mfma128" (128 x 128 tiles for every product), "mfma256" (256 x 256 tiles
+ * for every product with 16-byte aligned rows and no batch reduction, 128 x
+ * 128 for the rest), or "unavailable". The last two (also settable through
+ * VECTORCORE_HIP_GEMM) exist for tests and tuning: both tile sizes give the
+ * same bits for a product that neither splits along K. */
 const char* vc_hip_gemm_kernel(void);
-/* Selects the GEMM kernel for later calls: "mfma" or "simple". The reference
+/* Selects the GEMM kernel for later calls: "mfma", "simple", "mfma128" or
+ * "mfma256". The reference
  * picks its kernel once, from VECTORCORE_METAL_GEMM=tiled
  * (src/metal/metal_backend.mm:96-100), and re-runs its GEMM tests in a child
  * process to cover the portable one (tests/python/test_performance_paths.py:

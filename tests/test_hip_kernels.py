@@ -27,11 +27,14 @@ def device():
     C.synchronize()
 
 
-@pytest.fixture(params=["mfma", "simple"])
+@pytest.fixture(params=["mfma", "simple", "mfma256"])
 def gemm_kernel(request):
-    """Runs a GEMM test on the MFMA kernel and again on the portable FMA kernel
+    """Runs a GEMM test on the MFMA kernels, again on the portable FMA kernel
     (the reference re-runs its matmul tests with its portable kernel forced,
-    tests/python/test_performance_paths.py:89-103)."""
+    tests/python/test_performance_paths.py:89-103), and again with every
+    product whose operands allow it on the 256 x 256 tiles, so that their edges
+    (partial tiles, K past the last slice, split K) are checked on small
+    shapes too."""
     with C.gemm_kernel(request.param):
         assert C.lib().vc_hip_gemm_kernel().decode() == request.param
         yield request.param
@@ -156,6 +159,50 @@ def test_gemm_relu_mask_is_gemm_then_relu_backward_bitexact(gemm_kernel):
             C.check(C.lib().vc_hip_relu_backward(plain.ptr, dx.ptr, masked.ptr, batch * m * n))
             np.testing.assert_array_equal(fused.numpy(), masked.numpy(), err_msg=f"{m}x{k}x{n} ta={ta} tb={tb}")
             assert (fused.numpy() == 0).any() and (fused.numpy() != 0).any()
+
+
+# Shapes that run unsplit on both tile sizes: K below 4 slices of 32 (no split
+# for few tiles), or at least 256 tiles of 256 x 256 (a full round of
+# workgroups on either kernel); partial tiles along m and n, and K not a
+# multiple of the 32-deep slice.
+BIG_VS_128 = [(300, 96, 520), (1030, 64, 700), (260, 4, 8), (4096, 256, 4096), (4000, 200, 4100), (4100, 1028, 4096)]
+
+
+@pytest.mark.parametrize("m,k,n", BIG_VS_128)
+def test_big_tiles_give_the_bits_of_the_128_tiles(m, k, n):
+    """The 256 x 256 tiles compute each 64 x 64 block of C as a 128 x 128
+    tile's wave does (same MFMA blocks, lane layouts and k order), so products,
+    the fused ReLU mask, the bias + ReLU epilogue and the column-sum partial
+    rows are the same bits on both, in all four transposes."""
+    rng = np.random.default_rng(m + 3 * k + 5 * n)
+    x = rng.standard_normal((m, n)).astype(np.float32)
+    x.flat[:5] = [0.0, -0.0, np.nan, np.inf, -np.inf]
+    bias = rng.standard_normal(n).astype(np.float32)
+    dx, dbias = C.Buffer.of(x), C.Buffer.of(bias)
+    z0 = C.sizes([0])
+    for ta, tb in ((0, 0), (0, 1), (1, 0), (1, 1)):
+        a = rng.uniform(-1, 1, size=(k, m) if ta else (m, k)).astype(np.float32)
+        b = rng.uniform(-1, 1, size=(n, k) if tb else (k, n)).astype(np.float32)
+        da, db = C.Buffer.of(a), C.Buffer.of(b)
+        outs = {}
+        for kernel in ("mfma128", "mfma256"):
+            with C.gemm_kernel(kernel):
+                plain, masked, sums = C.Buffer((m, n)), C.Buffer((m, n)), C.Buffer((n,))
+                C.check(C.lib().vc_hip_matmul(da.ptr, db.ptr, plain.ptr, m, k, n, z0, z0, 1, ta, tb))
+                C.check(C.lib().vc_hip_matmul_relu_mask_colsum(da.ptr, db.ptr, masked.ptr, m, k, n, ta, tb, dx.ptr,
+                                                               sums.ptr))
+                outs[kernel] = [plain.numpy(), masked.numpy(), sums.numpy()]
+                if not ta and not tb:
+                    fwd = C.Buffer((m, n))
+                    C.check(C.lib().vc_hip_matmul_bias_relu(da.ptr, db.ptr, fwd.ptr, m, k, n, dbias.ptr, 1))
+                    outs[kernel].append(fwd.numpy())
+        for name, x128, x256 in zip(("product", "masked", "column sums", "bias + relu"), outs["mfma128"],
+                                    outs["mfma256"]):
+            np.testing.assert_array_equal(x256, x128, err_msg=f"{name} {m}x{k}x{n} ta={ta} tb={tb}")
+        rows = rng.choice(m, min(m, 48), replace=False)
+        opa = (a.T if ta else a)[rows]
+        np.testing.assert_allclose(outs["mfma256"][0][rows], K.matmul2d(np.ascontiguousarray(opa), b, False, bool(tb)),
+                                   rtol=1e-4, atol=1e-4 * np.sqrt(k))
 
 
 @pytest.mark.parametrize("m,k,n", [(300, 257, 130), (128, 64, 200), (100, 70, 33), (4096, 512, 1000),

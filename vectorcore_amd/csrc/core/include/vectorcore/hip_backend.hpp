@@ -28,7 +28,7 @@ public:
     [[nodiscard]] std::string last_error() const;
     // "mfma" (matrix-core tiles), "simple" (VECTORCORE_HIP_GEMM=simple) or "unavailable".
     [[nodiscard]] std::string gemm_kernel() const;
-    // "mfma" or "simple" for later products (vc_hip_set_gemm_kernel).
+    // "mfma", "simple", "mfma128" or "mfma256" for later products (vc_hip_set_gemm_kernel).
     void set_gemm_kernel(const std::string& name);
 
     // --- the reference device interface ---

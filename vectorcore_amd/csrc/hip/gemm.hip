@@ -41,6 +41,7 @@
 #include <limits>
 #include <optional>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 namespace vchip {
@@ -498,6 +499,398 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
     }
 }
 
+// ---- 256 x 256 tiles: one workgroup per CU, a 128 x 128 quadrant per wave ----
+//
+// Large products run on 256 x 256 tiles. Each of the four waves owns a
+// 128 x 128 quadrant as 2 x 2 blocks of 64 x 64, and computes each of them
+// exactly as gemm_mfma_kernel's wave computes its 64 x 64 (the same MFMA
+// blocks, the same lane layouts and the same k order), so C, the fused
+// epilogues and the column-sum partial rows (one per 64 rows) are the same
+// bits as on the 128 x 128 tiles. What changes is the work between barriers:
+// a wave issues 256 MFMAs per 32-deep slice instead of 64, and every LDS
+// fragment read feeds twice the MFMAs, so the slice barrier and the tile's
+// prologue are a quarter as frequent per MFMA. Two stages of [256][36] floats
+// per operand take 144 KiB of LDS: one workgroup, so one wave per SIMD, per
+// CU; the accumulators (256 per lane) live in the accumulation registers.
+// Vector (16-byte) loads only; misaligned operands stay on the 128 x 128 tiles.
+constexpr int BT = 256;
+constexpr int kBigSlots = BT * BK / (4 * kThreads);  // 16-byte loads per thread per operand slice (8)
+constexpr int kBigKcRows = kThreads / (BK / 4);      // k-contiguous rows one slot covers (32)
+constexpr int kBigMnRows = kThreads / (BT / 4);      // k-rows one slot of an m/n-contiguous operand covers (4)
+constexpr int kBigLdsTile = BT * (BK + kPadK);       // floats per operand stage: [256][32 + 4]
+static_assert(BK * BT <= kBigLdsTile, "m/n-contiguous tile larger than a stage");
+static_assert(kBigSlots == 8, "the slice schedule below stores 4 slots per k-group in groups 1 and 2");
+
+// Global -> register loader of a 256 (m/n) x 32 (k) operand tile in 8 slots
+// per thread. Slot q of a k-contiguous operand is row mn0 + 32 q, k
+// k0..k0+3 (8 threads per 32-float row); slot q of an m/n-contiguous operand
+// is k-row k0 + 4 q, columns mn0..mn0+3 (64 threads, one wave, per 256-float
+// row). Edges are masked as in TileLoader.
+template <bool KC>
+struct BigLoader {
+    const float* origin;
+    int64_t step;
+    int K, mn_lim;
+    uint32_t qstep, voff;
+    int mn0, k0;
+
+    __device__ void init(const float* base, int ld, int mn_origin, int MN, int K_) {
+        K = K_;
+        mn_lim = MN - mn_origin;
+        origin = KC ? base + int64_t(mn_origin) * ld : base + mn_origin;
+        step = KC ? int64_t(BK) : int64_t(BK) * ld;
+        const uint32_t ld4 = uint32_t(ld) * 4u;
+        const int t = threadIdx.x;
+        if (KC) {
+            mn0 = t / (BK / 4);
+            k0 = (t % (BK / 4)) * 4;
+            qstep = uint32_t(kBigKcRows) * ld4;
+        } else {
+            k0 = t / (BT / 4);
+            mn0 = (t % (BT / 4)) * 4;
+            qstep = uint32_t(kBigMnRows) * ld4;
+        }
+        voff = KC ? uint32_t(mn0) * ld4 + uint32_t(k0) * 4u : uint32_t(k0) * ld4 + uint32_t(mn0) * 4u;
+    }
+
+    __device__ __amdgpu_buffer_rsrc_t slice(int kt) const { return make_rsrc(origin + int64_t(kt) * step); }
+
+    __device__ f4 load(__amdgpu_buffer_rsrc_t rs, int kt, int q) const {
+        const int k = kt * BK + k0 + (KC ? 0 : kBigMnRows * q);
+        const int mn = mn0 + (KC ? kBigKcRows * q : 0);
+        const bool ok = mn < mn_lim && k < K;
+        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? voff : kOutOfRange,
+                                                                            uint32_t(q) * qstep, 0));
+    }
+
+    // Slot q's offset in a slice whose k all lie inside K: only rows
+    // (columns) past the matrix point out of range.
+    __device__ uint32_t full_slice_off(int q) const {
+        return mn0 + (KC ? kBigKcRows * q : 0) < mn_lim ? voff : kOutOfRange;
+    }
+    __device__ f4 load_at(__amdgpu_buffer_rsrc_t rs, uint32_t off, int q) const {
+        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, uint32_t(q) * qstep, 0));
+    }
+
+    __device__ uint32_t lds_off() const {
+        return KC ? uint32_t(mn0 * (BK + kPadK) + k0) * 4u : uint32_t(k0 * BT + mn0) * 4u;
+    }
+    static constexpr uint32_t lds_qstep = KC ? uint32_t(kBigKcRows) * (BK + kPadK) * 4u : uint32_t(kBigMnRows) * BT * 4u;
+};
+
+// One operand's fragments of one k-group for the wave's 128 rows: at(p, b, s)
+// is the value of 64-row half p, block b, for MFMA step s (as Frag, per half).
+template <bool KC>
+struct BigFrag;
+template <>
+struct BigFrag<true> {
+    f4 v[2][2];  // [half][block]
+    __device__ float at(int p, int b, int s) const { return v[p][b][s]; }
+};
+template <>
+struct BigFrag<false> {
+    f2 v[2][4];  // [half][step]
+    __device__ float at(int p, int b, int s) const { return v[p][s][b]; }
+};
+
+// Part s (0..3) of the fragments of k-group g for the wave's 128 rows at
+// `off`: a k-contiguous tile reads block (s / 2, s % 2) with one
+// ds_read_b128, an m/n-contiguous tile step s of both halves with two
+// ds_read_b64. Each half is read exactly as read_part reads a wave's 64 rows.
+template <bool KC>
+__device__ inline void big_read_part(const float* __restrict__ lds, int off, int g, int lane, int s,
+                                     BigFrag<KC>& frag) {
+    const int kb = g * 8 + 4 * (lane >> 5);
+    if constexpr (KC) {
+        const int p = s >> 1, b = s & 1;
+        frag.v[p][b] = *reinterpret_cast<const f4*>(lds + (off + 64 * p + 32 * b + (lane & 31)) * (BK + kPadK) + kb);
+    } else {
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+            frag.v[p][s] = *reinterpret_cast<const f2*>(lds + (kb + s) * BT + off + 64 * p + 2 * (lane & 31));
+    }
+}
+
+// The epilogue of one 64 x 64 block of C at tile rows wm.., columns wn..:
+// gemm_mfma_kernel's epilogue for one wave (ReLU mask, bias + ReLU, the
+// block's column-sum partial row `part_row`, the store), in the same order.
+template <bool AKC, bool BKC>
+__device__ inline void big_epilogue(const GemmArgs& p, f16v (&acc)[2][2], int64_t z, int64_t job, int m0, int n0,
+                                    int wm, int wn, int part_row) {
+    // The lane index is computed here (mbcnt) and passes through an empty asm
+    // statement, so neither it nor the per-element offsets below are kept
+    // across the K loop, where they would take registers the loop needs.
+    int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    asm volatile("" : "+v"(lane));
+    float* C = p.c + (p.splits > 1 ? job : z) * int64_t(p.M) * p.N;
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(C + int64_t(m0) * p.N + n0);
+    const bool masked = p.relu_mask && p.splits == 1;
+    const __amdgpu_buffer_rsrc_t rm =
+        make_rsrc((masked ? p.relu_mask + z * int64_t(p.M) * p.N : C) + int64_t(m0) * p.N + n0);
+    const int row_lim = p.M - m0, col_lim = p.N - n0;
+    const int row0 = wm + 4 * (lane >> 5), col0 = wn + (lane & 31);
+    const auto crow = [&](int i, int v) {
+        return AKC ? row0 + 32 * i + 8 * (v >> 2) + (v & 3) : wm + 2 * (8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) + i;
+    };
+    const auto ccol = [&](int j) { return BKC ? col0 + 32 * j : wn + 2 * (lane & 31) + j; };
+    if (masked) {  // 32 mask loads in flight at a time (all 64 would not fit beside the addresses)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            f16v x[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = ccol(j);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int row = crow(i, v);
+                    const bool ok = row < row_lim && col < col_lim;
+                    x[j][v] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rm, ok ? uint32_t(row * p.N + col) * 4u : kOutOfRange,
+                                                                    0, 0));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const float xv = x[j][v];
+                    const float value = acc[i][j][v];
+                    acc[i][j][v] = value * (xv > 0.0f ? 1.0f : 0.0f);
+                }
+        }
+    }
+    if (p.splits == 1 && (p.bias || p.relu)) {
+        float bias[2] = {0.0f, 0.0f};
+        if (p.bias) {
+            const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.bias + n0);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = ccol(j);
+                bias[j] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(rb, col < col_lim ? uint32_t(col) * 4u : kOutOfRange, 0, 0));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const float value = acc[i][j][v];
+                    acc[i][j][v] = bias_relu(value, bias[j], p.relu != 0);
+                }
+    }
+    // Partial rows past the 2 ceil(M / 128) that the 128 x 128 tiles write
+    // (and the caller allocates) lie wholly below C and are not written.
+    if (p.col_part && part_row < 2 * ((p.M + BM - 1) / BM)) {
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.col_part + int64_t(part_row) * p.N + n0);
+        const bool whole = row_lim >= wm + 64;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            double sum = 0.0;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const float value = acc[i][j][v];
+                    const int row = crow(i, v);
+                    sum += whole || row < row_lim ? double(value) : 0.0;
+                }
+            sum += __shfl_xor(sum, 32, 64);
+            const int col = ccol(j);
+            const uint64_t bits = __builtin_bit_cast(uint64_t, sum);
+            const uint32_t off = lane < 32 && col < col_lim ? uint32_t(col) * 8u : kOutOfRange;
+            __builtin_amdgcn_raw_buffer_store_b32(uint32_t(bits), rp, off, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(uint32_t(bits >> 32), rp, off + 4u, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = ccol(j);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = crow(i, v);
+                const bool ok = row < row_lim && col < col_lim;
+                const float value = acc[i][j][v];
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), rc,
+                                                      ok ? uint32_t(row * p.N + col) * 4u : kOutOfRange, 0, 0);
+            }
+        }
+}
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
+    // The slice schedule of gemm_mfma_kernel with twice the slots: step kt
+    // multiplies out of stage cur; k-groups 1 and 2 store slice kt + 1 (in
+    // registers since step kt - 1) into the other stage, four slots per
+    // operand each, and issue the loads of slice kt + 2 into the slots just
+    // stored; fragments are read one k-group ahead; one barrier before the
+    // fourth k-group's MFMAs, which overlap the reads of the next stage.
+    __shared__ __attribute__((aligned(16))) float As[2][kBigLdsTile];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kBigLdsTile];
+    constexpr bool AKC = !TA;
+    constexpr bool BKC = TB;
+    int tm, tn;
+    tile_coords(int(blockIdx.x), p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BT, n0 = tn * BT;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+    const int kt_total = (p.K + BK - 1) / BK;
+    // One job (output matrix, or split of one) per workgroup row of the grid,
+    // and no batch reduction: loops around the K loop here would make the
+    // register allocator spill.
+    {
+        const int64_t job = blockIdx.y;
+        const int64_t z = uniform64(job / p.splits);
+        const int split = __builtin_amdgcn_readfirstlane(int(job - z * p.splits));
+        const int kt_begin = split * p.kt_per_split;
+        const int kt_end = min(kt_total, kt_begin + p.kt_per_split);
+        const int64_t aoff = uniform64(p.table ? p.table[2 * z] : z * p.a_bstride);
+        const int64_t boff = uniform64(p.table ? p.table[2 * z + 1] : z * p.b_bstride);
+        f16v acc[2][2][2][2];  // [A half][B half][block i][block j]
+#pragma unroll
+        for (int ph = 0; ph < 2; ++ph)
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) acc[ph][qh][i][j][v] = 0.0f;
+
+        if (kt_begin < kt_end) {
+            BigLoader<AKC> la;
+            BigLoader<BKC> lb;
+            la.init(p.a + aoff, p.lda, m0, p.M, p.K);
+            lb.init(p.b + boff, p.ldb, n0, p.N, p.K);
+            f4 ra[kBigSlots], rb[kBigSlots];
+            char* const lds_a = reinterpret_cast<char*>(As[0]);
+            char* const lds_b = reinterpret_cast<char*>(Bs[0]);
+            const uint32_t a_st = la.lds_off(), b_st = lb.lds_off();
+            {
+                const __amdgpu_buffer_rsrc_t sa = la.slice(kt_begin), sb = lb.slice(kt_begin);
+#pragma unroll
+                for (int q = 0; q < kBigSlots; ++q) {
+                    ra[q] = la.load(sa, kt_begin, q);
+                    rb[q] = lb.load(sb, kt_begin, q);
+                }
+#pragma unroll
+                for (int q = 0; q < kBigSlots; ++q) {
+                    *reinterpret_cast<f4*>(lds_a + a_st + q * BigLoader<AKC>::lds_qstep) = ra[q];
+                    *reinterpret_cast<f4*>(lds_b + b_st + q * BigLoader<BKC>::lds_qstep) = rb[q];
+                }
+                const __amdgpu_buffer_rsrc_t na = la.slice(kt_begin + 1), nb = lb.slice(kt_begin + 1);
+#pragma unroll
+                for (int q = 0; q < kBigSlots; ++q) {
+                    ra[q] = la.load(na, kt_begin + 1, q);
+                    rb[q] = lb.load(nb, kt_begin + 1, q);
+                }
+            }
+            __syncthreads();
+            BigFrag<AKC> fa[2];  // [k-group parity]
+            BigFrag<BKC> fb[2];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                big_read_part<AKC>(As[0], wm, 0, lane, s, fa[0]);
+                big_read_part<BKC>(Bs[0], wn, 0, lane, s, fb[0]);
+            }
+            // Per-slot offsets of full slices (every k inside K): only the rows
+            // past the matrix are masked, once per tile. Steps whose loads are
+            // full slices use them, so their loop holds no vector ALU work
+            // (with one wave per SIMD each such instruction stalls the MFMA
+            // pipe); the last steps mask every load as TileLoader does.
+            uint32_t a_off[kBigSlots], b_off[kBigSlots];
+#pragma unroll
+            for (int q = 0; q < kBigSlots; ++q) {
+                a_off[q] = la.full_slice_off(q);
+                b_off[q] = lb.full_slice_off(q);
+            }
+            // One step. kFast: the loads (slice kt + 2) are full slices. kCur:
+            // the stage multiplied out of, 0 or 1 (known here, so every LDS
+            // address is a fixed offset from a per-lane base), or -1 (from kt).
+            const auto step = [&](auto fast_c, auto cur_c, int kt) {
+                constexpr bool kFast = decltype(fast_c)::value;
+                constexpr int kCur = decltype(cur_c)::value;
+                const int cur = kCur >= 0 ? kCur : (kt - kt_begin) & 1;
+                const float* as = As[cur];
+                const float* bs = Bs[cur];
+                const float* as_next = As[cur ^ 1];
+                const float* bs_next = Bs[cur ^ 1];
+                char* const st_a = lds_a + (cur ^ 1) * kBigLdsTile * 4;
+                char* const st_b = lds_b + (cur ^ 1) * kBigLdsTile * 4;
+                const __amdgpu_buffer_rsrc_t sa = la.slice(kt + 2), sb = lb.slice(kt + 2);
+#pragma unroll
+                for (int g = 0; g < BK / 8; ++g) {
+                    const int cb = g & 1;
+                    if (g == BK / 8 - 1) __syncthreads();
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        if (g == 1 || g == 2) {
+                            const int q = 4 * (g - 1) + s;
+                            *reinterpret_cast<f4*>(st_a + a_st + q * BigLoader<AKC>::lds_qstep) = ra[q];
+                            *reinterpret_cast<f4*>(st_b + b_st + q * BigLoader<BKC>::lds_qstep) = rb[q];
+                            ra[q] = kFast ? la.load_at(sa, a_off[q], q) : la.load(sa, kt + 2, q);
+                            rb[q] = kFast ? lb.load_at(sb, b_off[q], q) : lb.load(sb, kt + 2, q);
+                        }
+                        if (g + 1 < BK / 8) {
+                            big_read_part<AKC>(as, wm, g + 1, lane, s, fa[cb ^ 1]);
+                            big_read_part<BKC>(bs, wn, g + 1, lane, s, fb[cb ^ 1]);
+                        } else {
+                            big_read_part<AKC>(as_next, wm, 0, lane, s, fa[cb ^ 1]);
+                            big_read_part<BKC>(bs_next, wn, 0, lane, s, fb[cb ^ 1]);
+                        }
+#pragma unroll
+                        for (int ph = 0; ph < 2; ++ph)
+#pragma unroll
+                            for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+                                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                                    for (int j = 0; j < 2; ++j)
+                                        acc[ph][qh][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                            fa[cb].at(ph, i, s), fb[cb].at(qh, j, s), acc[ph][qh][i][j], 0, 0, 0);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+            };
+            // Pairs of steps whose loads are full slices of the range, then the
+            // rest one at a time. A pair starts on stage 0.
+            const int fast_end = min(kt_end, p.K / BK);
+            int kt = kt_begin;
+            for (; kt + 3 < fast_end; kt += 2) {
+                step(std::true_type{}, std::integral_constant<int, 0>{}, kt);
+                step(std::true_type{}, std::integral_constant<int, 1>{}, kt + 1);
+            }
+            for (; kt < kt_end; ++kt) step(std::false_type{}, std::integral_constant<int, -1>{}, kt);
+            __syncthreads();
+        }
+        // Each 64 x 64 block as gemm_mfma_kernel's wave finishes it; its
+        // column-sum partial row is the block's 64-row index in C.
+#pragma unroll
+        for (int ph = 0; ph < 2; ++ph)
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh) {
+                // One block at a time: its 64 values are copied out of the
+                // accumulation registers here (the empty asm pins the copy), so
+                // the epilogue's branches join vector registers, not the
+                // accumulators of the blocks still waiting.
+                f16v c[2][2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        c[i][j] = acc[ph][qh][i][j];
+                        asm volatile("" : "+v"(c[i][j]));
+                    }
+                big_epilogue<AKC, BKC>(p, c, z, job, m0, n0, wm + 64 * ph, wn + 64 * qh, (m0 + wm + 64 * ph) / 64);
+            }
+    }
+}
+
 // Split combine: c[z][i] = sum over s of part[z][s][i], in split order, then
 // the fused ReLU mask or the forward epilogue when there is one.
 __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ part, float* __restrict__ c,
@@ -807,8 +1200,11 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(GemmArgs p) {
 }
 
 template <bool TA, bool TB>
-void launch_variant(const GemmArgs& args, bool vec, bool simple, bool small, dim3 grid, hipStream_t stream) {
-    if (small) {
+void launch_variant(const GemmArgs& args, bool vec, bool simple, bool small, bool big, dim3 grid,
+                    hipStream_t stream) {
+    if (big) {
+        launch((gemm_big_kernel<TA, TB>), grid, dim3(kThreads), 0, stream, args);
+    } else if (small) {
         if (vec) launch((gemm_small_kernel<TA, TB, true>), grid, dim3(kSmallThreads), 0, stream, args);
         else launch((gemm_small_kernel<TA, TB, false>), grid, dim3(kSmallThreads), 0, stream, args);
     } else if (simple) {
@@ -844,6 +1240,28 @@ bool small_tiles(int64_t K, int64_t products, int64_t tiles128, bool tiny, bool 
     return work > 8 && work <= 32;
 }
 
+// Whether a product takes the 256 x 256 tiles (gemm_big_kernel) under the
+// automatic setting: a full round of workgroups (one per CU) and at least 32
+// K slices, or, where the 128 x 128 tiles would split K too (fewer than two
+// workgroups per CU), enough tiles to fill the CUs in four K ranges and K
+// long enough for ranges of 32 slices or more.
+// Measured on the MLP train step's products (MI355X, against the 128 x 128
+// tiles): 8192 x 4096 x 4096 NT 1914 -> 1841 us, 4096^2 x 8192 TN 1958 ->
+// 1845, 8192 x 4096 x 1024 NN 495 -> 486, 1024 x 4096 x 8192 TN 504 -> 497,
+// 4096 x 1000 x 8192 TN 504 -> 494; 8192 x 1000 x 4096 (128 tiles, which the
+// 128 x 128 tiles run unsplit) 484 -> 497, so it stays. A fused ReLU mask
+// adds its loads to the epilogue, which with one workgroup per CU nothing
+// overlaps: masked products need 64 slices (8192 x 4096 x 4096 masked NT
+// 1912 -> 1877 us; 8192 x 4096 x 1000 508 -> 527, so it stays).
+bool big_tiles(int64_t M, int64_t N, int64_t K, int64_t batch, int64_t reduce, int cu_count, bool masked) {
+    const int64_t tiles = ((M + BT - 1) / BT) * ((N + BT - 1) / BT) * batch;
+    const int64_t tiles128 = ((M + BM - 1) / BM) * ((N + BN - 1) / BN) * batch;
+    const int64_t slices = (K + BK - 1) / BK;
+    if (reduce != 1 || (masked && slices < 64)) return false;
+    return (tiles >= cu_count && slices >= 32) ||
+           (tiles128 < 2 * int64_t(cu_count) && 4 * tiles >= cu_count && slices >= 128);
+}
+
 // offsets: nullptr for the affine mode (a_bstride / b_bstride).
 void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t a_bstride,
           int64_t b_bstride, const std::vector<int64_t>* offsets, int64_t reduce, int64_t a_rstride, int64_t b_rstride,
@@ -857,14 +1275,21 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     if (pending && !column_sum) fail(VC_HIP_ERR_INVALID_ARGUMENT, "pending column sums need a column-sum buffer");
     if (M == 0 || N == 0 || batch == 0) return;
     if (!a || !b || !c) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul: null buffer");
-    const bool force_simple = d.simple_gemm.load();  // the kernel in force for this call
+    const int mode = d.gemm_mode.load();  // the kernel setting in force for this call
+    const bool force_simple = mode == kGemmSimple;
     // A single large NN product runs as NT on a transposed copy of B: the
-    // kernel is ~3.5% faster when both operands are contiguous along k, which
-    // outweighs the copy (2 K N floats of traffic) once M >= 4096. The LDS
-    // tiles, and so the bits, are those of the NN kernel. (K is bounded by the
-    // transpose's grid: 65535 tiles of 64 rows.)
+    // 128 x 128 tiles are ~3.5% faster when both operands are contiguous along
+    // k, which outweighs the copy (2 K N floats of traffic) once M >= 4096. The
+    // LDS tiles, and so the bits, are those of the NN kernel. (K is bounded by
+    // the transpose's grid: 65535 tiles of 64 rows.) On the 256 x 256 tiles NN
+    // is as fast as NT, and from K = 2048 on the copy no longer pays
+    // (8192 x 4096 x 4096: 1886 us with the copy, 1872 without; at K = 1024
+    // the copy still wins, 490 against 495).
+    const bool big_nn = (mode == kGemmTiles256 || (mode == kGemmAuto && K >= 2048 &&
+                                                   big_tiles(M, N, K, batch, reduce, d.cu_count, false))) &&
+                        std::max(K, N) * BT < (int64_t(1) << 29);
     if (!ta && !tb && batch == 1 && reduce == 1 && !force_simple && M >= kNnViaNtMinRows && N % 4 == 0 &&
-        K % 4 == 0 && K <= int64_t(65535) * 64 && aligned16(a) && aligned16(b) && !relu_mask) {
+        K % 4 == 0 && K <= int64_t(65535) * 64 && aligned16(a) && aligned16(b) && !relu_mask && !big_nn) {
         Profiled prof("gemm_nn", 2.0 * double(M) * double(N) * double(K),
                       4.0 * double(M * K + 2 * K * N + M * N) + (bias ? 4.0 * double(N) : 0.0));
         Scratch bt(size_t(K * N) * sizeof(float));
@@ -890,16 +1315,34 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     // the workgroup's eight waves (gemm_small_kernel): one launch, no split pass.
     // Its operand offsets are 32-bit from the operand's origin.
     const bool small_fits = M * K < (int64_t(1) << 29) && K * N < (int64_t(1) << 29) && M * N < (int64_t(1) << 29);
-    const bool small = !force_simple && small_fits && small_tiles(K, batch * reduce, tiles_m * tiles_n, tiny, ta, tb);
-    const bool simple = !small && (force_simple || tiny);
-    const int64_t tiles = small ? tiles_m32 * tiles_n32 : simple ? tiles_m_simple * tiles_n_simple : tiles_m * tiles_n;
-    if (tiles > std::numeric_limits<int>::max() / 2) fail(VC_HIP_ERR_OVERFLOW, "matmul output has too many tiles");
+    const bool automatic = mode == kGemmAuto;
+    bool small = automatic && small_fits && small_tiles(K, batch * reduce, tiles_m * tiles_n, tiny, ta, tb);
+    bool simple = force_simple || (automatic && !small && tiny);
     // Byte offsets relative to a tile origin are 32-bit: 128 rows of any
-    // operand or of C must span less than 2 GiB.
+    // operand or of C must span less than 2 GiB (256 rows for the 256 x 256 tiles).
     const int64_t kMax = int64_t(1) << 29;
     const int64_t widest = std::max({ta ? M : K, tb ? K : N, N});
     if (M >= kMax || N >= kMax || K >= kMax || widest * 128 >= kMax)
         fail(VC_HIP_ERR_OVERFLOW, "matmul operands exceed the 2 GiB per-matrix addressing of the HIP kernels");
+    // 16-byte vector loads need every row start and batch offset on a 4-float boundary.
+    bool vec = aligned16(a) && aligned16(b) && (ta ? M : K) % 4 == 0 && (tb ? K : N) % 4 == 0 && a_rstride % 4 == 0 &&
+               b_rstride % 4 == 0;
+    if (offsets) {
+        for (int64_t v : *offsets) vec = vec && v % 4 == 0;
+    } else {
+        vec = vec && a_bstride % 4 == 0 && b_bstride % 4 == 0;
+    }
+    const int64_t tiles_m256 = (M + BT - 1) / BT, tiles_n256 = (N + BT - 1) / BT;
+    const bool big_fits = vec && widest * BT < kMax && reduce == 1 && batch <= 65535 / 32;
+    const bool big = big_fits && (mode == kGemmTiles256 ||
+                                  (automatic && !small && !simple &&
+                                   big_tiles(M, N, K, batch, reduce, d.cu_count, relu_mask != nullptr)));
+    if (big) small = simple = false;
+    const int64_t tiles = big     ? tiles_m256 * tiles_n256
+                          : small ? tiles_m32 * tiles_n32
+                          : simple ? tiles_m_simple * tiles_n_simple
+                                   : tiles_m * tiles_n;
+    if (tiles > std::numeric_limits<int>::max() / 2) fail(VC_HIP_ERR_OVERFLOW, "matmul output has too many tiles");
 
     GemmArgs args{};
     args.a = a;
@@ -916,23 +1359,17 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     args.reduce = reduce;
     args.a_rstride = a_rstride;
     args.b_rstride = b_rstride;
-    args.tiles_m = int(small ? tiles_m32 : simple ? tiles_m_simple : tiles_m);
-    args.tiles_n = int(small ? tiles_n32 : simple ? tiles_n_simple : tiles_n);
+    args.tiles_m = int(big ? tiles_m256 : small ? tiles_m32 : simple ? tiles_m_simple : tiles_m);
+    args.tiles_n = int(big ? tiles_n256 : small ? tiles_n32 : simple ? tiles_n_simple : tiles_n);
 
-    // 16-byte vector loads need every row start and batch offset on a 4-float boundary.
-    bool vec = aligned16(a) && aligned16(b) && args.lda % 4 == 0 && args.ldb % 4 == 0 && a_rstride % 4 == 0 &&
-               b_rstride % 4 == 0;
     Scratch table(offsets ? offsets->size() * sizeof(int64_t) : 8);
     if (offsets) {
-        for (int64_t v : *offsets) vec = vec && v % 4 == 0;
         const int rc = vc_hip_upload(table.as<void>(), offsets->data(), offsets->size() * sizeof(int64_t));
         if (rc != VC_HIP_OK) fail(rc, "matmul offset table upload failed");
         args.table = table.as<int64_t>();
-    } else {
-        vec = vec && a_bstride % 4 == 0 && b_bstride % 4 == 0;
     }
-    // Split the work when the output has fewer tiles than two workgroups per
-    // CU: a batch reduction (reduce > 1) splits into ranges of r, a long K into
+    // Split the work when the output has fewer tiles than workgroup slots
+    // (two per CU on the 128 x 128 tiles, one on the 256 x 256): a batch reduction (reduce > 1) splits into ranges of r, a long K into
     // ranges of at least 32 slices (16 for 65 to 128 tiles; at most 4 ranges), and the K of a tiny output
     // (<= kTinyTiles tiles) into up to 32 ranges. Each split accumulates into
     // its own partial matrix and a second pass sums the partials in split
@@ -940,8 +1377,9 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     const int kt_total = int((K + BK - 1) / BK);
     int splits = 1;
     int64_t r_per_split = reduce;
-    const int64_t want = (2 * int64_t(d.cu_count) + tiles * batch - 1) / (tiles * batch);
-    if (!simple && !small && tiles * batch < 2 * int64_t(d.cu_count)) {
+    const int64_t slots = (big ? 1 : 2) * int64_t(d.cu_count);
+    const int64_t want = (slots + tiles * batch - 1) / (tiles * batch);
+    if (!simple && !small && tiles * batch < slots) {
         if (reduce > 1) {
             r_per_split = (reduce + std::min(want, reduce) - 1) / std::min(want, reduce);
             splits = int((reduce + r_per_split - 1) / r_per_split);
@@ -952,7 +1390,7 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
         } else if (kt_total >= 64) {
             splits = int(std::min<int64_t>(want, 4));
             splits = std::min(splits, kt_total / 32);
-        } else if (4 * tiles * batch <= 2 * int64_t(d.cu_count) && kt_total >= 32) {
+        } else if (4 * tiles * batch <= slots && kt_total >= 32) {
             // 65 to 128 tiles (fewer take the 32 x 32 tiles) with K of 1024
             // to 2047 fill at most a quarter of the workgroup slots: ranges of
             // at least 16 slices fill them (2048 x 1024 x 1024: 72 -> 50 us;
@@ -988,10 +1426,10 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
         (bias ? 4.0 * double(N) : 0.0);
     std::optional<Profiled> prof;
     if (!in_caller_scope) prof.emplace(label, flops, bytes);
-    if (ta && tb) launch_variant<true, true>(args, vec, simple, small, grid, d.stream);
-    else if (ta) launch_variant<true, false>(args, vec, simple, small, grid, d.stream);
-    else if (tb) launch_variant<false, true>(args, vec, simple, small, grid, d.stream);
-    else launch_variant<false, false>(args, vec, simple, small, grid, d.stream);
+    if (ta && tb) launch_variant<true, true>(args, vec, simple, small, big, grid, d.stream);
+    else if (ta) launch_variant<true, false>(args, vec, simple, small, big, grid, d.stream);
+    else if (tb) launch_variant<false, true>(args, vec, simple, small, big, grid, d.stream);
+    else launch_variant<false, false>(args, vec, simple, small, big, grid, d.stream);
     if (splits > 1) {
         after_launch(label);
         const int64_t total = batch * M * N;

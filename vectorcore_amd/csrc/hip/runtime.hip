@@ -59,7 +59,8 @@ void init_device(Device& d) {
     d.name += std::string(" (") + prop.gcnArchName + ")";
     d.cu_count = prop.multiProcessorCount;
     d.sync_each_launch = env_is("VECTORCORE_HIP_SYNC_EACH", "1");
-    d.simple_gemm = env_is("VECTORCORE_HIP_GEMM", "simple");
+    for (int mode : {kGemmSimple, kGemmTiles128, kGemmTiles256})
+        if (env_is("VECTORCORE_HIP_GEMM", gemm_mode_name(mode))) d.gemm_mode = mode;
     d.ready = true;
 }
 
@@ -356,6 +357,15 @@ void pool_release(void* p) noexcept {
     }
 }
 
+const char* gemm_mode_name(int mode) {
+    switch (mode) {
+        case kGemmSimple: return "simple";
+        case kGemmTiles128: return "mfma128";
+        case kGemmTiles256: return "mfma256";
+        default: return "mfma";
+    }
+}
+
 Device& device() {
     static std::once_flag once;
     Device& d = device_singleton();
@@ -528,16 +538,19 @@ const char* vc_hip_last_error(void) {
 const char* vc_hip_gemm_kernel(void) {
     Device& d = device();
     if (!d.ready) return "unavailable";
-    return d.simple_gemm ? "simple" : "mfma";
+    return gemm_mode_name(d.gemm_mode.load());
 }
 
 int vc_hip_set_gemm_kernel(const char* name) {
     return guard([&] {
         Device& d = require_device();
-        if (name && std::strcmp(name, "mfma") == 0) d.simple_gemm = false;
-        else if (name && std::strcmp(name, "simple") == 0) d.simple_gemm = true;
-        else fail(VC_HIP_ERR_INVALID_ARGUMENT, std::string("unknown GEMM kernel '") + (name ? name : "(null)") +
-                                                   "': expected \"mfma\" or \"simple\"");
+        for (int mode : {kGemmAuto, kGemmSimple, kGemmTiles128, kGemmTiles256})
+            if (name && std::strcmp(name, gemm_mode_name(mode)) == 0) {
+                d.gemm_mode = mode;
+                return;
+            }
+        fail(VC_HIP_ERR_INVALID_ARGUMENT, std::string("unknown GEMM kernel '") + (name ? name : "(null)") +
+                                              "': expected \"mfma\", \"simple\", \"mfma128\" or \"mfma256\"");
     });
 }
 

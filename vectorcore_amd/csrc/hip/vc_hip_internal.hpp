@@ -79,8 +79,17 @@ struct Device {
     int cu_count = 0;
     hipStream_t stream = nullptr;
     bool sync_each_launch = false;  // VECTORCORE_HIP_SYNC_EACH=1 (fault localisation)
-    std::atomic<bool> simple_gemm{false};  // VECTORCORE_HIP_GEMM=simple or vc_hip_set_gemm_kernel
+    std::atomic<int> gemm_mode{0};  // a GemmMode: VECTORCORE_HIP_GEMM or vc_hip_set_gemm_kernel
 };
+
+// GEMM kernel selection (vc_hip_set_gemm_kernel names in brackets): automatic
+// ("mfma": the FMA kernel for tiny products, 32 x 32, 128 x 128 or 256 x 256
+// matrix-core tiles by shape), the portable FMA kernel for every product
+// ("simple"), the 128 x 128 tiles for every product ("mfma128"), or the
+// 256 x 256 tiles for every product whose operands allow them, the 128 x 128
+// tiles for the rest ("mfma256").
+enum GemmMode : int { kGemmAuto = 0, kGemmSimple = 1, kGemmTiles128 = 2, kGemmTiles256 = 3 };
+const char* gemm_mode_name(int mode);
 
 // Initialises once (thread-safe) and makes the device current on this thread.
 Device& device();

@@ -117,6 +117,16 @@ __device__ inline void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, i
     tn = local / group_rows;
 }
 
+// f(std::integral_constant<int, i>) for i = 0 .. N - 1, in order, with i a
+// constant expression inside f.
+template <int N, typename F, int I = 0>
+__device__ inline void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, F, I + 1>(static_cast<F&&>(f));
+    }
+}
+
 __device__ inline int64_t uniform64(int64_t v) {
     const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(uint64_t(v)));
     const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(uint64_t(v) >> 32));
@@ -127,6 +137,10 @@ __device__ inline int64_t uniform64(int64_t v) {
 // kOutOfRange fall outside num_records: loads return 0, stores are dropped.
 // The raw buffer builtins move 32-bit integers; values are bit-cast.
 constexpr uint32_t kOutOfRange = 0x80000000u;
+// s_waitcnt immediate (gfx9 encoding) that waits for every vector memory
+// operation (vmcnt 0) and no other counter: loads that write LDS directly
+// must land before the barrier that hands their stage to the other waves.
+constexpr int kWaitVmcnt0 = 0x0F70;
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), short(0), int(kOutOfRange - 1), 0x00020000);
 }
@@ -508,74 +522,93 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
 // epilogues and the column-sum partial rows (one per 64 rows) are the same
 // bits as on the 128 x 128 tiles. What changes is the work between barriers:
 // a wave issues 256 MFMAs per 32-deep slice instead of 64, and every LDS
-// fragment read feeds twice the MFMAs, so the slice barrier and the tile's
-// prologue are a quarter as frequent per MFMA. Two stages of [256][36] floats
-// per operand take 144 KiB of LDS: one workgroup, so one wave per SIMD, per
-// CU; the accumulators (256 per lane) live in the accumulation registers.
-// Vector (16-byte) loads only; misaligned operands stay on the 128 x 128 tiles.
+// fragment read feeds twice the MFMAs. One workgroup, so one wave per SIMD,
+// per CU; the accumulators (256 per lane) live in the accumulation registers.
+// With one wave per SIMD nothing hides an instruction that holds up the
+// MFMAs, so operand slices go from memory straight into LDS (16-byte buffer
+// loads with the LDS destination: no staging registers, no LDS store
+// instructions; those stores alone cost 3% of the K loop), and the loop holds
+// no vector ALU work. Two stages of two unpadded 32 KiB tiles: 128 KiB of
+// LDS. Vector (16-byte) loads only; misaligned operands stay on the 128 x 128
+// tiles.
 constexpr int BT = 256;
 constexpr int kBigSlots = BT * BK / (4 * kThreads);  // 16-byte loads per thread per operand slice (8)
-constexpr int kBigKcRows = kThreads / (BK / 4);      // k-contiguous rows one slot covers (32)
-constexpr int kBigMnRows = kThreads / (BT / 4);      // k-rows one slot of an m/n-contiguous operand covers (4)
-constexpr int kBigLdsTile = BT * (BK + kPadK);       // floats per operand stage: [256][32 + 4]
-static_assert(BK * BT <= kBigLdsTile, "m/n-contiguous tile larger than a stage");
-static_assert(kBigSlots == 8, "the slice schedule below stores 4 slots per k-group in groups 1 and 2");
+constexpr int kBigLdsTile = BT * BK;                 // floats per operand stage (32 KiB)
+static_assert(kBigSlots == 8, "the slice schedule loads 4 slots per operand in k-groups 0 and 1");
 
-// Global -> register loader of a 256 (m/n) x 32 (k) operand tile in 8 slots
-// per thread. Slot q of a k-contiguous operand is row mn0 + 32 q, k
-// k0..k0+3 (8 threads per 32-float row); slot q of an m/n-contiguous operand
-// is k-row k0 + 4 q, columns mn0..mn0+3 (64 threads, one wave, per 256-float
-// row). Edges are masked as in TileLoader.
+// LDS pointer for the loads that write LDS directly.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Memory -> LDS loader of a 256 (m/n) x 32 (k) operand slice: 8 loads per
+// thread, each writing its wave's 1 KiB contiguously (lane t at byte 16 t of
+// the load's LDS destination, which is uniform per wave).
+// - k-contiguous operand ([256][32] in LDS): load q of wave w covers rows
+//   32 q + 8 w .. + 7, 8 lanes per 32-float row. Lane t writes 16-byte chunk
+//   t % 8 of its row r and fetches into it the row's chunk (t % 8) ^ (r / 2 % 8)
+//   (k = 4 x chunk): chunk c of row r lies at c ^ (r / 2 % 8), so the
+//   fragment reads (16 consecutive rows at one k) hit 16 different bank groups.
+// - m/n-contiguous operand ([32][256]): load q of wave w covers k-row w + 4 q,
+//   lane t its columns 4 t .. 4 t + 3.
+// Edges: rows (columns) past the matrix, and k past K, point out of range;
+// such lanes write zeros into LDS.
 template <bool KC>
 struct BigLoader {
     const float* origin;
     int64_t step;
-    int K, mn_lim;
-    uint32_t qstep, voff;
-    int mn0, k0;
+    int K, mn_lim, wave;
+    uint32_t qstep, voff;  // soffset step per load; this lane's byte offset of load 0 in a slice
+    int mn0, k0;           // this lane's row (column) and k of load 0, from the slice origin
 
-    __device__ void init(const float* base, int ld, int mn_origin, int MN, int K_) {
+    __device__ void init(const float* base, int ld, int mn_origin, int MN, int K_, int wave_, int lane) {
         K = K_;
         mn_lim = MN - mn_origin;
+        wave = wave_;
         origin = KC ? base + int64_t(mn_origin) * ld : base + mn_origin;
         step = KC ? int64_t(BK) : int64_t(BK) * ld;
         const uint32_t ld4 = uint32_t(ld) * 4u;
-        const int t = threadIdx.x;
         if (KC) {
-            mn0 = t / (BK / 4);
-            k0 = (t % (BK / 4)) * 4;
-            qstep = uint32_t(kBigKcRows) * ld4;
+            mn0 = 8 * wave + lane / 8;
+            k0 = 4 * ((lane % 8) ^ ((mn0 >> 1) & 7));
+            qstep = 32u * ld4;
         } else {
-            k0 = t / (BT / 4);
-            mn0 = (t % (BT / 4)) * 4;
-            qstep = uint32_t(kBigMnRows) * ld4;
+            k0 = wave;
+            mn0 = 4 * lane;
+            qstep = 4u * ld4;
         }
         voff = KC ? uint32_t(mn0) * ld4 + uint32_t(k0) * 4u : uint32_t(k0) * ld4 + uint32_t(mn0) * 4u;
     }
 
     __device__ __amdgpu_buffer_rsrc_t slice(int kt) const { return make_rsrc(origin + int64_t(kt) * step); }
 
-    __device__ f4 load(__amdgpu_buffer_rsrc_t rs, int kt, int q) const {
-        const int k = kt * BK + k0 + (KC ? 0 : kBigMnRows * q);
-        const int mn = mn0 + (KC ? kBigKcRows * q : 0);
-        const bool ok = mn < mn_lim && k < K;
-        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? voff : kOutOfRange,
-                                                                            uint32_t(q) * qstep, 0));
+    // Load q's offset in slice kt, every edge masked.
+    __device__ uint32_t masked_off(int kt, int q) const {
+        const int k = kt * BK + k0 + (KC ? 0 : 4 * q);
+        const int mn = mn0 + (KC ? 32 * q : 0);
+        return mn < mn_lim && k < K ? voff : kOutOfRange;
     }
-
-    // Slot q's offset in a slice whose k all lie inside K: only rows
+    // Load q's offset in a slice whose k all lie inside K: only rows
     // (columns) past the matrix point out of range.
-    __device__ uint32_t full_slice_off(int q) const {
-        return mn0 + (KC ? kBigKcRows * q : 0) < mn_lim ? voff : kOutOfRange;
-    }
-    __device__ f4 load_at(__amdgpu_buffer_rsrc_t rs, uint32_t off, int q) const {
-        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, uint32_t(q) * qstep, 0));
-    }
+    __device__ uint32_t full_slice_off(int q) const { return mn0 + (KC ? 32 * q : 0) < mn_lim ? voff : kOutOfRange; }
 
-    __device__ uint32_t lds_off() const {
-        return KC ? uint32_t(mn0 * (BK + kPadK) + k0) * 4u : uint32_t(k0 * BT + mn0) * 4u;
+    // Issue load q of the slice at rs into the LDS stage at `stage`. Written
+    // as inline assembly so that the compiler does not see an LDS write: it
+    // cannot always tell which LDS array such a load writes, and would then
+    // wait for every load in flight before unrelated LDS reads. The loads are
+    // waited for explicitly (kWaitVmcnt0) before the barrier that publishes
+    // their stage; the compiler's own vmcnt waits only ever wait for more.
+    // The LDS destination is this wave's base in the stage plus a constant
+    // per load, added in the statement itself, so that one base per stage is
+    // kept rather than one address per load.
+    template <int Q>
+    __device__ void load(__amdgpu_buffer_rsrc_t rs, float* stage, uint32_t off) const {
+        constexpr uint32_t dst_q = KC ? uint32_t(32 * Q) * (BK * 4) : uint32_t(4 * Q) * (BT * 4);
+        const uint32_t base = uint32_t(reinterpret_cast<uintptr_t>((lds_ptr_t)stage)) +
+                              (KC ? uint32_t(8 * wave) * (BK * 4) : uint32_t(wave) * (BT * 4));
+        asm volatile("s_add_u32 m0, %0, %4\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                     :
+                     : "s"(base), "v"(off), "s"(rs), "s"(uint32_t(Q) * qstep), "i"(dst_q)
+                     : "memory", "m0", "scc");
     }
-    static constexpr uint32_t lds_qstep = KC ? uint32_t(kBigKcRows) * (BK + kPadK) * 4u : uint32_t(kBigMnRows) * BT * 4u;
 };
 
 // One operand's fragments of one k-group for the wave's 128 rows: at(p, b, s)
@@ -595,69 +628,96 @@ struct BigFrag<false> {
 
 // Part s (0..3) of the fragments of k-group g for the wave's 128 rows at
 // `off`: a k-contiguous tile reads block (s / 2, s % 2) with one
-// ds_read_b128, an m/n-contiguous tile step s of both halves with two
-// ds_read_b64. Each half is read exactly as read_part reads a wave's 64 rows.
+// ds_read_b128 (k 8 g + 4 h .. + 3 for half-wave h: chunk 2 g + h, found at
+// (2 g + h) ^ (row / 2 % 8), and row / 2 % 8 = lane / 2 % 8 here), an
+// m/n-contiguous tile step s of both halves with two ds_read_b64. Each half
+// holds what read_part gives a wave's 64 rows.
 template <bool KC>
 __device__ inline void big_read_part(const float* __restrict__ lds, int off, int g, int lane, int s,
                                      BigFrag<KC>& frag) {
-    const int kb = g * 8 + 4 * (lane >> 5);
     if constexpr (KC) {
         const int p = s >> 1, b = s & 1;
-        frag.v[p][b] = *reinterpret_cast<const f4*>(lds + (off + 64 * p + 32 * b + (lane & 31)) * (BK + kPadK) + kb);
+        const int chunk = (2 * g + (lane >> 5)) ^ ((lane >> 1) & 7);
+        frag.v[p][b] = *reinterpret_cast<const f4*>(lds + (off + 64 * p + 32 * b + (lane & 31)) * BK + 4 * chunk);
     } else {
+        const int kb = g * 8 + 4 * (lane >> 5);
 #pragma unroll
         for (int p = 0; p < 2; ++p)
             frag.v[p][s] = *reinterpret_cast<const f2*>(lds + (kb + s) * BT + off + 64 * p + 2 * (lane & 31));
     }
 }
 
+// The lane index, computed where it is used (mbcnt) and passed through an
+// empty asm statement, so that neither it nor the per-element offsets derived
+// from it are kept across the K loop, where they would take registers the
+// loop needs.
+__device__ inline int epilogue_lane() {
+    int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    asm volatile("" : "+v"(lane));
+    return lane;
+}
+
+// Tile coordinates of accumulator value v of block (i, j) of the 64 x 64
+// block at tile rows wm.., columns wn.. (D row d = 8 (v / 4) + 4 (lane / 32)
+// + v % 4, column lane % 32; a k-contiguous operand's blocks are 32
+// consecutive rows (columns), an m/n-contiguous one's interleave).
+template <bool AKC, bool BKC>
+struct BlockCoords {
+    int wm, wn, lane;
+    __device__ int row(int i, int v) const {
+        return AKC ? wm + 4 * (lane >> 5) + 32 * i + 8 * (v >> 2) + (v & 3)
+                   : wm + 2 * (8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) + i;
+    }
+    __device__ int col(int j) const { return BKC ? wn + (lane & 31) + 32 * j : wn + 2 * (lane & 31) + j; }
+};
+
+// Issues the loads of the ReLU mask under the 64 x 64 block at tile rows
+// wm.., columns wn.. (one per accumulator value; outside C they read 0).
+template <bool AKC, bool BKC>
+__device__ inline void big_mask_load(const GemmArgs& p, int64_t z, int m0, int n0, int wm, int wn,
+                                     f16v (&x)[2][2]) {
+    const BlockCoords<AKC, BKC> bc{wm, wn, epilogue_lane()};
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(p.relu_mask + z * int64_t(p.M) * p.N + int64_t(m0) * p.N + n0);
+    const int row_lim = p.M - m0, col_lim = p.N - n0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = bc.col(j);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = bc.row(i, v);
+                const bool ok = row < row_lim && col < col_lim;
+                x[i][j][v] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(rm, ok ? uint32_t(row * p.N + col) * 4u : kOutOfRange, 0, 0));
+            }
+        }
+}
+
 // The epilogue of one 64 x 64 block of C at tile rows wm.., columns wn..:
 // gemm_mfma_kernel's epilogue for one wave (ReLU mask, bias + ReLU, the
 // block's column-sum partial row `part_row`, the store), in the same order.
+// The mask values come loaded (big_mask_load) when the product has one.
 template <bool AKC, bool BKC>
-__device__ inline void big_epilogue(const GemmArgs& p, f16v (&acc)[2][2], int64_t z, int64_t job, int m0, int n0,
-                                    int wm, int wn, int part_row) {
-    // The lane index is computed here (mbcnt) and passes through an empty asm
-    // statement, so neither it nor the per-element offsets below are kept
-    // across the K loop, where they would take registers the loop needs.
-    int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-    asm volatile("" : "+v"(lane));
+__device__ inline void big_epilogue(const GemmArgs& p, f16v (&acc)[2][2], const f16v (&mask)[2][2], int64_t z,
+                                    int64_t job, int m0, int n0, int wm, int wn, int part_row) {
+    const BlockCoords<AKC, BKC> bc{wm, wn, epilogue_lane()};
+    const int lane = bc.lane;
     float* C = p.c + (p.splits > 1 ? job : z) * int64_t(p.M) * p.N;
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(C + int64_t(m0) * p.N + n0);
     const bool masked = p.relu_mask && p.splits == 1;
-    const __amdgpu_buffer_rsrc_t rm =
-        make_rsrc((masked ? p.relu_mask + z * int64_t(p.M) * p.N : C) + int64_t(m0) * p.N + n0);
     const int row_lim = p.M - m0, col_lim = p.N - n0;
-    const int row0 = wm + 4 * (lane >> 5), col0 = wn + (lane & 31);
-    const auto crow = [&](int i, int v) {
-        return AKC ? row0 + 32 * i + 8 * (v >> 2) + (v & 3) : wm + 2 * (8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) + i;
-    };
-    const auto ccol = [&](int j) { return BKC ? col0 + 32 * j : wn + 2 * (lane & 31) + j; };
-    if (masked) {  // 32 mask loads in flight at a time (all 64 would not fit beside the addresses)
+    if (masked) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            f16v x[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int col = ccol(j);
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int row = crow(i, v);
-                    const bool ok = row < row_lim && col < col_lim;
-                    x[j][v] = __builtin_bit_cast(
-                        float, __builtin_amdgcn_raw_buffer_load_b32(rm, ok ? uint32_t(row * p.N + col) * 4u : kOutOfRange,
-                                                                    0, 0));
-                }
-            }
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const float xv = x[j][v];
+                    const float xv = mask[i][j][v];
                     const float value = acc[i][j][v];
                     acc[i][j][v] = value * (xv > 0.0f ? 1.0f : 0.0f);
                 }
-        }
     }
     if (p.splits == 1 && (p.bias || p.relu)) {
         float bias[2] = {0.0f, 0.0f};
@@ -665,7 +725,7 @@ __device__ inline void big_epilogue(const GemmArgs& p, f16v (&acc)[2][2], int64_
             const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.bias + n0);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int col = ccol(j);
+                const int col = bc.col(j);
                 bias[j] = __builtin_bit_cast(
                     float, __builtin_amdgcn_raw_buffer_load_b32(rb, col < col_lim ? uint32_t(col) * 4u : kOutOfRange, 0, 0));
             }
@@ -693,11 +753,11 @@ __device__ inline void big_epilogue(const GemmArgs& p, f16v (&acc)[2][2], int64_
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const float value = acc[i][j][v];
-                    const int row = crow(i, v);
+                    const int row = bc.row(i, v);
                     sum += whole || row < row_lim ? double(value) : 0.0;
                 }
             sum += __shfl_xor(sum, 32, 64);
-            const int col = ccol(j);
+            const int col = bc.col(j);
             const uint64_t bits = __builtin_bit_cast(uint64_t, sum);
             const uint32_t off = lane < 32 && col < col_lim ? uint32_t(col) * 8u : kOutOfRange;
             __builtin_amdgcn_raw_buffer_store_b32(uint32_t(bits), rp, off, 0, 0);
@@ -708,10 +768,10 @@ __device__ inline void big_epilogue(const GemmArgs& p, f16v (&acc)[2][2], int64_
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int col = ccol(j);
+            const int col = bc.col(j);
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int row = crow(i, v);
+                const int row = bc.row(i, v);
                 const bool ok = row < row_lim && col < col_lim;
                 const float value = acc[i][j][v];
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), rc,
@@ -722,14 +782,16 @@ __device__ inline void big_epilogue(const GemmArgs& p, f16v (&acc)[2][2], int64_
 
 template <bool TA, bool TB>
 __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
-    // The slice schedule of gemm_mfma_kernel with twice the slots: step kt
-    // multiplies out of stage cur; k-groups 1 and 2 store slice kt + 1 (in
-    // registers since step kt - 1) into the other stage, four slots per
-    // operand each, and issue the loads of slice kt + 2 into the slots just
-    // stored; fragments are read one k-group ahead; one barrier before the
-    // fourth k-group's MFMAs, which overlap the reads of the next stage.
-    __shared__ __attribute__((aligned(16))) float As[2][kBigLdsTile];
-    __shared__ __attribute__((aligned(16))) float Bs[2][kBigLdsTile];
+    // Step kt multiplies out of stage cur while k-groups 0 and 1 issue the
+    // loads of slice kt + 1 into the other stage (free since the previous
+    // step's barrier), four per operand each; fragments are read one k-group
+    // ahead; before the fourth k-group the loads are waited for and one
+    // barrier makes the other stage complete, and the fourth k-group's MFMAs
+    // overlap the reads of its first fragments.
+    __shared__ __attribute__((aligned(16))) float A0[kBigLdsTile];
+    __shared__ __attribute__((aligned(16))) float A1[kBigLdsTile];
+    __shared__ __attribute__((aligned(16))) float B0[kBigLdsTile];
+    __shared__ __attribute__((aligned(16))) float B1[kBigLdsTile];
     constexpr bool AKC = !TA;
     constexpr bool BKC = TB;
     int tm, tn;
@@ -750,6 +812,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
         const int kt_end = min(kt_total, kt_begin + p.kt_per_split);
         const int64_t aoff = uniform64(p.table ? p.table[2 * z] : z * p.a_bstride);
         const int64_t boff = uniform64(p.table ? p.table[2 * z + 1] : z * p.b_bstride);
+        const bool masked = p.relu_mask && p.splits == 1;
+        f16v mk[2][2][2];      // fused ReLU mask of a block of C: [block parity][i][j]
         f16v acc[2][2][2][2];  // [A half][B half][block i][block j]
 #pragma unroll
         for (int ph = 0; ph < 2; ++ph)
@@ -765,76 +829,64 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
         if (kt_begin < kt_end) {
             BigLoader<AKC> la;
             BigLoader<BKC> lb;
-            la.init(p.a + aoff, p.lda, m0, p.M, p.K);
-            lb.init(p.b + boff, p.ldb, n0, p.N, p.K);
-            f4 ra[kBigSlots], rb[kBigSlots];
-            char* const lds_a = reinterpret_cast<char*>(As[0]);
-            char* const lds_b = reinterpret_cast<char*>(Bs[0]);
-            const uint32_t a_st = la.lds_off(), b_st = lb.lds_off();
+            la.init(p.a + aoff, p.lda, m0, p.M, p.K, wave, lane);
+            lb.init(p.b + boff, p.ldb, n0, p.N, p.K, wave, lane);
             {
                 const __amdgpu_buffer_rsrc_t sa = la.slice(kt_begin), sb = lb.slice(kt_begin);
-#pragma unroll
-                for (int q = 0; q < kBigSlots; ++q) {
-                    ra[q] = la.load(sa, kt_begin, q);
-                    rb[q] = lb.load(sb, kt_begin, q);
-                }
-#pragma unroll
-                for (int q = 0; q < kBigSlots; ++q) {
-                    *reinterpret_cast<f4*>(lds_a + a_st + q * BigLoader<AKC>::lds_qstep) = ra[q];
-                    *reinterpret_cast<f4*>(lds_b + b_st + q * BigLoader<BKC>::lds_qstep) = rb[q];
-                }
-                const __amdgpu_buffer_rsrc_t na = la.slice(kt_begin + 1), nb = lb.slice(kt_begin + 1);
-#pragma unroll
-                for (int q = 0; q < kBigSlots; ++q) {
-                    ra[q] = la.load(na, kt_begin + 1, q);
-                    rb[q] = lb.load(nb, kt_begin + 1, q);
-                }
+                static_for<kBigSlots>([&](auto qc) {
+                    constexpr int q = decltype(qc)::value;
+                    la.template load<q>(sa, A0, la.masked_off(kt_begin, q));
+                    lb.template load<q>(sb, B0, lb.masked_off(kt_begin, q));
+                });
             }
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
             __syncthreads();
             BigFrag<AKC> fa[2];  // [k-group parity]
             BigFrag<BKC> fb[2];
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                big_read_part<AKC>(As[0], wm, 0, lane, s, fa[0]);
-                big_read_part<BKC>(Bs[0], wn, 0, lane, s, fb[0]);
+                big_read_part<AKC>(A0, wm, 0, lane, s, fa[0]);
+                big_read_part<BKC>(B0, wn, 0, lane, s, fb[0]);
             }
-            // Per-slot offsets of full slices (every k inside K): only the rows
-            // past the matrix are masked, once per tile. Steps whose loads are
-            // full slices use them, so their loop holds no vector ALU work
-            // (with one wave per SIMD each such instruction stalls the MFMA
-            // pipe); the last steps mask every load as TileLoader does.
+            // Per-load offsets of full slices (every k inside K): only the
+            // rows past the matrix are masked, once per tile. Steps whose
+            // loads are full slices use them, so their loop holds no vector
+            // ALU work; the last steps mask every load.
             uint32_t a_off[kBigSlots], b_off[kBigSlots];
 #pragma unroll
             for (int q = 0; q < kBigSlots; ++q) {
                 a_off[q] = la.full_slice_off(q);
                 b_off[q] = lb.full_slice_off(q);
             }
-            // One step. kFast: the loads (slice kt + 2) are full slices. kCur:
-            // the stage multiplied out of, 0 or 1 (known here, so every LDS
-            // address is a fixed offset from a per-lane base), or -1 (from kt).
+            // One step. kFast: its loads (slice kt + 1) are a full slice of the
+            // range. kCur: the stage multiplied out of, 0 or 1 (known here, so
+            // every LDS address is a fixed offset from a per-lane base), or -1
+            // (from kt).
             const auto step = [&](auto fast_c, auto cur_c, int kt) {
                 constexpr bool kFast = decltype(fast_c)::value;
                 constexpr int kCur = decltype(cur_c)::value;
                 const int cur = kCur >= 0 ? kCur : (kt - kt_begin) & 1;
-                const float* as = As[cur];
-                const float* bs = Bs[cur];
-                const float* as_next = As[cur ^ 1];
-                const float* bs_next = Bs[cur ^ 1];
-                char* const st_a = lds_a + (cur ^ 1) * kBigLdsTile * 4;
-                char* const st_b = lds_b + (cur ^ 1) * kBigLdsTile * 4;
-                const __amdgpu_buffer_rsrc_t sa = la.slice(kt + 2), sb = lb.slice(kt + 2);
-#pragma unroll
-                for (int g = 0; g < BK / 8; ++g) {
+                const float* as = cur ? A1 : A0;
+                const float* bs = cur ? B1 : B0;
+                float* const as_next = cur ? A0 : A1;
+                float* const bs_next = cur ? B0 : B1;
+                const bool more = kFast || kt + 1 < kt_end;
+                const __amdgpu_buffer_rsrc_t sa = la.slice(kt + 1), sb = lb.slice(kt + 1);
+                static_for<BK / 8>([&](auto gc) {
+                    constexpr int g = decltype(gc)::value;
                     const int cb = g & 1;
-                    if (g == BK / 8 - 1) __syncthreads();
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) {
-                        if (g == 1 || g == 2) {
-                            const int q = 4 * (g - 1) + s;
-                            *reinterpret_cast<f4*>(st_a + a_st + q * BigLoader<AKC>::lds_qstep) = ra[q];
-                            *reinterpret_cast<f4*>(st_b + b_st + q * BigLoader<BKC>::lds_qstep) = rb[q];
-                            ra[q] = kFast ? la.load_at(sa, a_off[q], q) : la.load(sa, kt + 2, q);
-                            rb[q] = kFast ? lb.load_at(sb, b_off[q], q) : lb.load(sb, kt + 2, q);
+                    if (g == BK / 8 - 1) {
+                        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+                        __syncthreads();
+                    }
+                    static_for<4>([&](auto sc) {
+                        constexpr int s = decltype(sc)::value;
+                        if constexpr (g <= 1) {
+                            constexpr int q = 4 * g + s;
+                            if (more) {
+                                la.template load<q>(sa, as_next, kFast ? a_off[q] : la.masked_off(kt + 1, q));
+                                lb.template load<q>(sb, bs_next, kFast ? b_off[q] : lb.masked_off(kt + 1, q));
+                            }
                         }
                         if (g + 1 < BK / 8) {
                             big_read_part<AKC>(as, wm, g + 1, lane, s, fa[cb ^ 1]);
@@ -854,14 +906,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
                                         acc[ph][qh][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
                                             fa[cb].at(ph, i, s), fb[cb].at(qh, j, s), acc[ph][qh][i][j], 0, 0, 0);
                         __builtin_amdgcn_sched_barrier(0);
-                    }
-                }
+                    });
+                });
             };
             // Pairs of steps whose loads are full slices of the range, then the
             // rest one at a time. A pair starts on stage 0.
             const int fast_end = min(kt_end, p.K / BK);
             int kt = kt_begin;
-            for (; kt + 3 < fast_end; kt += 2) {
+            for (; kt + 2 < fast_end; kt += 2) {
                 step(std::true_type{}, std::integral_constant<int, 0>{}, kt);
                 step(std::true_type{}, std::integral_constant<int, 1>{}, kt + 1);
             }
@@ -869,11 +921,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
             __syncthreads();
         }
         // Each 64 x 64 block as gemm_mfma_kernel's wave finishes it; its
-        // column-sum partial row is the block's 64-row index in C.
+        // column-sum partial row is the block's 64-row index in C. A fused
+        // ReLU mask is loaded one block ahead (two register sets), so only the
+        // first block waits for its whole load latency.
+        if (masked) big_mask_load<AKC, BKC>(p, z, m0, n0, wm, wn, mk[0]);
 #pragma unroll
         for (int ph = 0; ph < 2; ++ph)
 #pragma unroll
             for (int qh = 0; qh < 2; ++qh) {
+                const int blk = 2 * ph + qh;
+                if (masked && blk < 3)
+                    big_mask_load<AKC, BKC>(p, z, m0, n0, wm + 64 * ((blk + 1) >> 1), wn + 64 * ((blk + 1) & 1),
+                                            mk[(blk + 1) & 1]);
                 // One block at a time: its 64 values are copied out of the
                 // accumulation registers here (the empty asm pins the copy), so
                 // the epilogue's branches join vector registers, not the
@@ -886,7 +945,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
                         c[i][j] = acc[ph][qh][i][j];
                         asm volatile("" : "+v"(c[i][j]));
                     }
-                big_epilogue<AKC, BKC>(p, c, z, job, m0, n0, wm + 64 * ph, wn + 64 * qh, (m0 + wm + 64 * ph) / 64);
+                big_epilogue<AKC, BKC>(p, c, mk[(2 * ph + qh) & 1], z, job, m0, n0, wm + 64 * ph, wn + 64 * qh,
+                                       (m0 + wm + 64 * ph) / 64);
             }
     }
 }

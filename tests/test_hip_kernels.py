@@ -27,14 +27,14 @@ def device():
     C.synchronize()
 
 
-@pytest.fixture(params=["mfma", "simple", "mfma256"])
+@pytest.fixture(params=["mfma", "simple", "mfma256", "mfma256x128"])
 def gemm_kernel(request):
     """Runs a GEMM test on the MFMA kernels, again on the portable FMA kernel
     (the reference re-runs its matmul tests with its portable kernel forced,
     tests/python/test_performance_paths.py:89-103), and again with every
-    product whose operands allow it on the 256 x 256 tiles, so that their edges
-    (partial tiles, K past the last slice, split K) are checked on small
-    shapes too."""
+    product whose operands allow it on the 256 x 256 and on the 256 x 128
+    tiles, so that their edges (partial tiles, K past the last slice, split K)
+    are checked on small shapes too."""
     with C.gemm_kernel(request.param):
         assert C.lib().vc_hip_gemm_kernel().decode() == request.param
         yield request.param
@@ -170,10 +170,10 @@ BIG_VS_128 = [(300, 96, 520), (1030, 64, 700), (260, 4, 8), (4096, 256, 4096), (
 
 @pytest.mark.parametrize("m,k,n", BIG_VS_128)
 def test_big_tiles_give_the_bits_of_the_128_tiles(m, k, n):
-    """The 256 x 256 tiles compute each 64 x 64 block of C as a 128 x 128
-    tile's wave does (same MFMA blocks, lane layouts and k order), so products,
-    the fused ReLU mask, the bias + ReLU epilogue and the column-sum partial
-    rows are the same bits on both, in all four transposes."""
+    """The 256 x 256 and 256 x 128 tiles compute each 64 x 64 block of C as a
+    128 x 128 tile's wave does (same MFMA blocks, lane layouts and k order), so
+    products, the fused ReLU mask, the bias + ReLU epilogue and the column-sum
+    partial rows are the same bits on all three, in all four transposes."""
     rng = np.random.default_rng(m + 3 * k + 5 * n)
     x = rng.standard_normal((m, n)).astype(np.float32)
     x.flat[:5] = [0.0, -0.0, np.nan, np.inf, -np.inf]
@@ -185,7 +185,7 @@ def test_big_tiles_give_the_bits_of_the_128_tiles(m, k, n):
         b = rng.uniform(-1, 1, size=(n, k) if tb else (k, n)).astype(np.float32)
         da, db = C.Buffer.of(a), C.Buffer.of(b)
         outs = {}
-        for kernel in ("mfma128", "mfma256"):
+        for kernel in ("mfma128", "mfma256", "mfma256x128"):
             with C.gemm_kernel(kernel):
                 plain, masked, sums = C.Buffer((m, n)), C.Buffer((m, n)), C.Buffer((n,))
                 C.check(C.lib().vc_hip_matmul(da.ptr, db.ptr, plain.ptr, m, k, n, z0, z0, 1, ta, tb))
@@ -196,9 +196,10 @@ def test_big_tiles_give_the_bits_of_the_128_tiles(m, k, n):
                     fwd = C.Buffer((m, n))
                     C.check(C.lib().vc_hip_matmul_bias_relu(da.ptr, db.ptr, fwd.ptr, m, k, n, dbias.ptr, 1))
                     outs[kernel].append(fwd.numpy())
-        for name, x128, x256 in zip(("product", "masked", "column sums", "bias + relu"), outs["mfma128"],
-                                    outs["mfma256"]):
-            np.testing.assert_array_equal(x256, x128, err_msg=f"{name} {m}x{k}x{n} ta={ta} tb={tb}")
+        for big in ("mfma256", "mfma256x128"):
+            for name, x128, xbig in zip(("product", "masked", "column sums", "bias + relu"), outs["mfma128"],
+                                        outs[big]):
+                np.testing.assert_array_equal(xbig, x128, err_msg=f"{big}: {name} {m}x{k}x{n} ta={ta} tb={tb}")
         rows = rng.choice(m, min(m, 48), replace=False)
         opa = (a.T if ta else a)[rows]
         np.testing.assert_allclose(outs["mfma256"][0][rows], K.matmul2d(np.ascontiguousarray(opa), b, False, bool(tb)),

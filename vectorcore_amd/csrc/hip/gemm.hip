@@ -531,28 +531,29 @@ __global__ __launch_bounds__(kThreads, Vec ? 2 : 1) void gemm_mfma_kernel(GemmAr
 // no vector ALU work. Two stages of two unpadded 32 KiB tiles: 128 KiB of
 // LDS. Vector (16-byte) loads only; misaligned operands stay on the 128 x 128
 // tiles.
-constexpr int BT = 256;
-constexpr int kBigSlots = BT * BK / (4 * kThreads);  // 16-byte loads per thread per operand slice (8)
-constexpr int kBigLdsTile = BT * BK;                 // floats per operand stage (32 KiB)
-static_assert(kBigSlots == 8, "the slice schedule loads 4 slots per operand in k-groups 0 and 1");
+constexpr int BT = 256;                   // tile rows (M); tile columns BN_ = 256 or 128
+constexpr int kBigLdsTile = BT * BK;       // floats per operand stage at most (32 KiB)
 
 // LDS pointer for the loads that write LDS directly.
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// Memory -> LDS loader of a 256 (m/n) x 32 (k) operand slice: 8 loads per
-// thread, each writing its wave's 1 KiB contiguously (lane t at byte 16 t of
-// the load's LDS destination, which is uniform per wave).
-// - k-contiguous operand ([256][32] in LDS): load q of wave w covers rows
+// Memory -> LDS loader of an EXT (m/n; 256 or 128) x 32 (k) operand slice:
+// EXT / 32 loads per thread, each writing its wave's 1 KiB contiguously
+// (lane t at byte 16 t of the load's LDS destination, which is uniform per
+// wave; load q of wave w lands at byte 1024 w + 4096 q of the stage).
+// - k-contiguous operand ([EXT][32] in LDS): load q of wave w covers rows
 //   32 q + 8 w .. + 7, 8 lanes per 32-float row. Lane t writes 16-byte chunk
 //   t % 8 of its row r and fetches into it the row's chunk (t % 8) ^ (r / 2 % 8)
 //   (k = 4 x chunk): chunk c of row r lies at c ^ (r / 2 % 8), so the
 //   fragment reads (16 consecutive rows at one k) hit 16 different bank groups.
-// - m/n-contiguous operand ([32][256]): load q of wave w covers k-row w + 4 q,
-//   lane t its columns 4 t .. 4 t + 3.
+// - m/n-contiguous operand ([32][EXT]): load q of wave w covers the 256 / EXT
+//   k-rows from (1024 / EXT) q + (256 / EXT) w, lane t column 4 t mod EXT.
 // Edges: rows (columns) past the matrix, and k past K, point out of range;
 // such lanes write zeros into LDS.
-template <bool KC>
+template <bool KC, int EXT>
 struct BigLoader {
+    static constexpr int kSlots = EXT / 32;        // loads per thread per slice
+    static constexpr int kRowsPerLoad = 1024 / EXT;  // k-rows of an m/n-contiguous operand per load round
     const float* origin;
     int64_t step;
     int K, mn_lim, wave;
@@ -571,9 +572,9 @@ struct BigLoader {
             k0 = 4 * ((lane % 8) ^ ((mn0 >> 1) & 7));
             qstep = 32u * ld4;
         } else {
-            k0 = wave;
-            mn0 = 4 * lane;
-            qstep = 4u * ld4;
+            k0 = (256 / EXT) * wave + lane / (EXT / 4);
+            mn0 = 4 * (lane % (EXT / 4));
+            qstep = uint32_t(kRowsPerLoad) * ld4;
         }
         voff = KC ? uint32_t(mn0) * ld4 + uint32_t(k0) * 4u : uint32_t(k0) * ld4 + uint32_t(mn0) * 4u;
     }
@@ -582,7 +583,7 @@ struct BigLoader {
 
     // Load q's offset in slice kt, every edge masked.
     __device__ uint32_t masked_off(int kt, int q) const {
-        const int k = kt * BK + k0 + (KC ? 0 : 4 * q);
+        const int k = kt * BK + k0 + (KC ? 0 : kRowsPerLoad * q);
         const int mn = mn0 + (KC ? 32 * q : 0);
         return mn < mn_lim && k < K ? voff : kOutOfRange;
     }
@@ -601,9 +602,8 @@ struct BigLoader {
     // kept rather than one address per load.
     template <int Q>
     __device__ void load(__amdgpu_buffer_rsrc_t rs, float* stage, uint32_t off) const {
-        constexpr uint32_t dst_q = KC ? uint32_t(32 * Q) * (BK * 4) : uint32_t(4 * Q) * (BT * 4);
-        const uint32_t base = uint32_t(reinterpret_cast<uintptr_t>((lds_ptr_t)stage)) +
-                              (KC ? uint32_t(8 * wave) * (BK * 4) : uint32_t(wave) * (BT * 4));
+        constexpr uint32_t dst_q = 4096u * Q;
+        const uint32_t base = uint32_t(reinterpret_cast<uintptr_t>((lds_ptr_t)stage)) + 1024u * uint32_t(wave);
         asm volatile("s_add_u32 m0, %0, %4\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                      :
                      : "s"(base), "v"(off), "s"(rs), "s"(uint32_t(Q) * qstep), "i"(dst_q)
@@ -626,24 +626,25 @@ struct BigFrag<false> {
     __device__ float at(int p, int b, int s) const { return v[p][s][b]; }
 };
 
-// Part s (0..3) of the fragments of k-group g for the wave's 128 rows at
-// `off`: a k-contiguous tile reads block (s / 2, s % 2) with one
-// ds_read_b128 (k 8 g + 4 h .. + 3 for half-wave h: chunk 2 g + h, found at
-// (2 g + h) ^ (row / 2 % 8), and row / 2 % 8 = lane / 2 % 8 here), an
-// m/n-contiguous tile step s of both halves with two ds_read_b64. Each half
-// holds what read_part gives a wave's 64 rows.
-template <bool KC>
+// Part s (0..3) of the fragments of k-group g for the wave's NP 64-row halves
+// at `off` of a tile EXT wide along m/n: a k-contiguous tile reads block
+// (s / 2, s % 2) with one ds_read_b128 (k 8 g + 4 h .. + 3 for half-wave h:
+// chunk 2 g + h, found at (2 g + h) ^ (row / 2 % 8), and row / 2 % 8 =
+// lane / 2 % 8 here), an m/n-contiguous tile step s of each half with one
+// ds_read_b64. Each half holds what read_part gives a wave's 64 rows.
+template <bool KC, int EXT, int NP>
 __device__ inline void big_read_part(const float* __restrict__ lds, int off, int g, int lane, int s,
                                      BigFrag<KC>& frag) {
     if constexpr (KC) {
         const int p = s >> 1, b = s & 1;
         const int chunk = (2 * g + (lane >> 5)) ^ ((lane >> 1) & 7);
-        frag.v[p][b] = *reinterpret_cast<const f4*>(lds + (off + 64 * p + 32 * b + (lane & 31)) * BK + 4 * chunk);
+        if (p < NP)
+            frag.v[p][b] = *reinterpret_cast<const f4*>(lds + (off + 64 * p + 32 * b + (lane & 31)) * BK + 4 * chunk);
     } else {
         const int kb = g * 8 + 4 * (lane >> 5);
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
-            frag.v[p][s] = *reinterpret_cast<const f2*>(lds + (kb + s) * BT + off + 64 * p + 2 * (lane & 31));
+        for (int p = 0; p < NP; ++p)
+            frag.v[p][s] = *reinterpret_cast<const f2*>(lds + (kb + s) * EXT + off + 64 * p + 2 * (lane & 31));
     }
 }
 
@@ -780,7 +781,7 @@ __device__ inline void big_epilogue(const GemmArgs& p, f16v (&acc)[2][2], const 
         }
 }
 
-template <bool TA, bool TB>
+template <bool TA, bool TB, int BN_>
 __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
     // Step kt multiplies out of stage cur while k-groups 0 and 1 issue the
     // loads of slice kt + 1 into the other stage (free since the previous
@@ -790,16 +791,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
     // overlap the reads of its first fragments.
     __shared__ __attribute__((aligned(16))) float A0[kBigLdsTile];
     __shared__ __attribute__((aligned(16))) float A1[kBigLdsTile];
-    __shared__ __attribute__((aligned(16))) float B0[kBigLdsTile];
-    __shared__ __attribute__((aligned(16))) float B1[kBigLdsTile];
+    __shared__ __attribute__((aligned(16))) float B0[BN_ * BK];
+    __shared__ __attribute__((aligned(16))) float B1[BN_ * BK];
     constexpr bool AKC = !TA;
     constexpr bool BKC = TB;
+    constexpr int QN = BN_ / 128;  // 64-column halves per wave
+    using LoaderA = BigLoader<AKC, BT>;
+    using LoaderB = BigLoader<BKC, BN_>;
     int tm, tn;
     tile_coords(int(blockIdx.x), p.tiles_m, p.tiles_n, tm, tn);
-    const int m0 = tm * BT, n0 = tn * BT;
+    const int m0 = tm * BT, n0 = tn * BN_;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
-    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * (BN_ / 2);
     const int kt_total = (p.K + BK - 1) / BK;
     // One job (output matrix, or split of one) per workgroup row of the grid,
     // and no batch reduction: loops around the K loop here would make the
@@ -813,12 +817,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
         const int64_t aoff = uniform64(p.table ? p.table[2 * z] : z * p.a_bstride);
         const int64_t boff = uniform64(p.table ? p.table[2 * z + 1] : z * p.b_bstride);
         const bool masked = p.relu_mask && p.splits == 1;
-        f16v mk[2][2][2];      // fused ReLU mask of a block of C: [block parity][i][j]
-        f16v acc[2][2][2][2];  // [A half][B half][block i][block j]
+        f16v mk[2][2][2];       // fused ReLU mask of a block of C: [block parity][i][j]
+        f16v acc[2][QN][2][2];  // [A half][B half][block i][block j]
 #pragma unroll
         for (int ph = 0; ph < 2; ++ph)
 #pragma unroll
-            for (int qh = 0; qh < 2; ++qh)
+            for (int qh = 0; qh < QN; ++qh)
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -827,16 +831,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
                         for (int v = 0; v < 16; ++v) acc[ph][qh][i][j][v] = 0.0f;
 
         if (kt_begin < kt_end) {
-            BigLoader<AKC> la;
-            BigLoader<BKC> lb;
+            LoaderA la;
+            LoaderB lb;
             la.init(p.a + aoff, p.lda, m0, p.M, p.K, wave, lane);
             lb.init(p.b + boff, p.ldb, n0, p.N, p.K, wave, lane);
             {
                 const __amdgpu_buffer_rsrc_t sa = la.slice(kt_begin), sb = lb.slice(kt_begin);
-                static_for<kBigSlots>([&](auto qc) {
+                static_for<LoaderA::kSlots>([&](auto qc) {
                     constexpr int q = decltype(qc)::value;
                     la.template load<q>(sa, A0, la.masked_off(kt_begin, q));
-                    lb.template load<q>(sb, B0, lb.masked_off(kt_begin, q));
+                    if constexpr (q < LoaderB::kSlots) lb.template load<q>(sb, B0, lb.masked_off(kt_begin, q));
                 });
             }
             __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
@@ -845,19 +849,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
             BigFrag<BKC> fb[2];
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                big_read_part<AKC>(A0, wm, 0, lane, s, fa[0]);
-                big_read_part<BKC>(B0, wn, 0, lane, s, fb[0]);
+                big_read_part<AKC, BT, 2>(A0, wm, 0, lane, s, fa[0]);
+                big_read_part<BKC, BN_, QN>(B0, wn, 0, lane, s, fb[0]);
             }
             // Per-load offsets of full slices (every k inside K): only the
             // rows past the matrix are masked, once per tile. Steps whose
             // loads are full slices use them, so their loop holds no vector
             // ALU work; the last steps mask every load.
-            uint32_t a_off[kBigSlots], b_off[kBigSlots];
+            uint32_t a_off[LoaderA::kSlots], b_off[LoaderB::kSlots];
 #pragma unroll
-            for (int q = 0; q < kBigSlots; ++q) {
-                a_off[q] = la.full_slice_off(q);
-                b_off[q] = lb.full_slice_off(q);
-            }
+            for (int q = 0; q < LoaderA::kSlots; ++q) a_off[q] = la.full_slice_off(q);
+#pragma unroll
+            for (int q = 0; q < LoaderB::kSlots; ++q) b_off[q] = lb.full_slice_off(q);
             // One step. kFast: its loads (slice kt + 1) are a full slice of the
             // range. kCur: the stage multiplied out of, 0 or 1 (known here, so
             // every LDS address is a fixed offset from a per-lane base), or -1
@@ -885,20 +888,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
                             constexpr int q = 4 * g + s;
                             if (more) {
                                 la.template load<q>(sa, as_next, kFast ? a_off[q] : la.masked_off(kt + 1, q));
-                                lb.template load<q>(sb, bs_next, kFast ? b_off[q] : lb.masked_off(kt + 1, q));
+                                if constexpr (q < LoaderB::kSlots)
+                                    lb.template load<q>(sb, bs_next, kFast ? b_off[q] : lb.masked_off(kt + 1, q));
                             }
                         }
                         if (g + 1 < BK / 8) {
-                            big_read_part<AKC>(as, wm, g + 1, lane, s, fa[cb ^ 1]);
-                            big_read_part<BKC>(bs, wn, g + 1, lane, s, fb[cb ^ 1]);
+                            big_read_part<AKC, BT, 2>(as, wm, g + 1, lane, s, fa[cb ^ 1]);
+                            big_read_part<BKC, BN_, QN>(bs, wn, g + 1, lane, s, fb[cb ^ 1]);
                         } else {
-                            big_read_part<AKC>(as_next, wm, 0, lane, s, fa[cb ^ 1]);
-                            big_read_part<BKC>(bs_next, wn, 0, lane, s, fb[cb ^ 1]);
+                            big_read_part<AKC, BT, 2>(as_next, wm, 0, lane, s, fa[cb ^ 1]);
+                            big_read_part<BKC, BN_, QN>(bs_next, wn, 0, lane, s, fb[cb ^ 1]);
                         }
 #pragma unroll
                         for (int ph = 0; ph < 2; ++ph)
 #pragma unroll
-                            for (int qh = 0; qh < 2; ++qh)
+                            for (int qh = 0; qh < QN; ++qh)
 #pragma unroll
                                 for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -928,10 +932,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
 #pragma unroll
         for (int ph = 0; ph < 2; ++ph)
 #pragma unroll
-            for (int qh = 0; qh < 2; ++qh) {
-                const int blk = 2 * ph + qh;
-                if (masked && blk < 3)
-                    big_mask_load<AKC, BKC>(p, z, m0, n0, wm + 64 * ((blk + 1) >> 1), wn + 64 * ((blk + 1) & 1),
+            for (int qh = 0; qh < QN; ++qh) {
+                const int blk = QN * ph + qh;
+                if (masked && blk + 1 < 2 * QN)
+                    big_mask_load<AKC, BKC>(p, z, m0, n0, wm + 64 * ((blk + 1) / QN), wn + 64 * ((blk + 1) % QN),
                                             mk[(blk + 1) & 1]);
                 // One block at a time: its 64 values are copied out of the
                 // accumulation registers here (the empty asm pins the copy), so
@@ -945,7 +949,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
                         c[i][j] = acc[ph][qh][i][j];
                         asm volatile("" : "+v"(c[i][j]));
                     }
-                big_epilogue<AKC, BKC>(p, c, mk[(2 * ph + qh) & 1], z, job, m0, n0, wm + 64 * ph, wn + 64 * qh,
+                big_epilogue<AKC, BKC>(p, c, mk[blk & 1], z, job, m0, n0, wm + 64 * ph, wn + 64 * qh,
                                        (m0 + wm + 64 * ph) / 64);
             }
     }
@@ -1260,10 +1264,12 @@ __global__ __launch_bounds__(kSmallThreads) void gemm_small_kernel(GemmArgs p) {
 }
 
 template <bool TA, bool TB>
-void launch_variant(const GemmArgs& args, bool vec, bool simple, bool small, bool big, dim3 grid,
+void launch_variant(const GemmArgs& args, bool vec, bool simple, bool small, int big_n, dim3 grid,
                     hipStream_t stream) {
-    if (big) {
-        launch((gemm_big_kernel<TA, TB>), grid, dim3(kThreads), 0, stream, args);
+    if (big_n == 256) {
+        launch((gemm_big_kernel<TA, TB, 256>), grid, dim3(kThreads), 0, stream, args);
+    } else if (big_n == 128) {
+        launch((gemm_big_kernel<TA, TB, 128>), grid, dim3(kThreads), 0, stream, args);
     } else if (small) {
         if (vec) launch((gemm_small_kernel<TA, TB, true>), grid, dim3(kSmallThreads), 0, stream, args);
         else launch((gemm_small_kernel<TA, TB, false>), grid, dim3(kSmallThreads), 0, stream, args);
@@ -1300,26 +1306,33 @@ bool small_tiles(int64_t K, int64_t products, int64_t tiles128, bool tiny, bool 
     return work > 8 && work <= 32;
 }
 
-// Whether a product takes the 256 x 256 tiles (gemm_big_kernel) under the
-// automatic setting: a full round of workgroups (one per CU) and at least 32
-// K slices, or, where the 128 x 128 tiles would split K too (fewer than two
-// workgroups per CU), enough tiles to fill the CUs in four K ranges and K
-// long enough for ranges of 32 slices or more.
-// Measured on the MLP train step's products (MI355X, against the 128 x 128
-// tiles): 8192 x 4096 x 4096 NT 1914 -> 1841 us, 4096^2 x 8192 TN 1958 ->
-// 1845, 8192 x 4096 x 1024 NN 495 -> 486, 1024 x 4096 x 8192 TN 504 -> 497,
-// 4096 x 1000 x 8192 TN 504 -> 494; 8192 x 1000 x 4096 (128 tiles, which the
-// 128 x 128 tiles run unsplit) 484 -> 497, so it stays. A fused ReLU mask
-// adds its loads to the epilogue, which with one workgroup per CU nothing
-// overlaps: masked products need 64 slices (8192 x 4096 x 4096 masked NT
-// 1912 -> 1877 us; 8192 x 4096 x 1000 508 -> 527, so it stays).
-bool big_tiles(int64_t M, int64_t N, int64_t K, int64_t batch, int64_t reduce, int cu_count, bool masked) {
+// The tile width of gemm_big_kernel (256 or 128 columns of 256 rows) for a
+// product under the automatic setting, or 0 for the other kernels, from
+// measurements on MI355X against the 128 x 128 tiles:
+// - a full round of 256 x 256 tiles (one workgroup per CU) and at least 32 K
+//   slices: 256 (8192 x 4096 x 4096 NT 1914 -> 1807 us, 4096^2 x 8192 TN
+//   1958 -> 1807, 8192 x 4096 x 1024 NN 495 -> 477);
+// - else a full round of 256 x 128 tiles: 128 (8192 x 1000 x 4096 NN 485 ->
+//   458; 8 x 1024^3 NT 128 -> 124, TN 134 -> 127);
+// - where the 128 x 128 tiles would split K (fewer than two workgroups per
+//   CU): 256 x 128 tiles split in two (4096 x 1000 x 8192 TN 504 -> 469,
+//   1024 x 4096 x 8192 TN 504 -> 469; 256 x 256 tiles split in four took
+//   482 and 485), or 256 x 256 tiles split in four.
+// A fused ReLU mask adds its loads to the epilogue, which with one workgroup
+// per CU nothing overlaps and every CU reaches at once: masked products need 64
+// slices (8192 x 4096 x 4096 masked NT 1915 -> 1846 us; 8192 x 4096 x 1000
+// 508 -> 518, so it stays).
+int big_tiles(int64_t M, int64_t N, int64_t K, int64_t batch, int64_t reduce, int cu_count, bool masked) {
     const int64_t tiles = ((M + BT - 1) / BT) * ((N + BT - 1) / BT) * batch;
+    const int64_t tiles_half = ((M + BT - 1) / BT) * ((N + 127) / 128) * batch;
     const int64_t tiles128 = ((M + BM - 1) / BM) * ((N + BN - 1) / BN) * batch;
     const int64_t slices = (K + BK - 1) / BK;
-    if (reduce != 1 || (masked && slices < 64)) return false;
-    return (tiles >= cu_count && slices >= 32) ||
-           (tiles128 < 2 * int64_t(cu_count) && 4 * tiles >= cu_count && slices >= 128);
+    if (reduce != 1 || (masked && slices < 64)) return 0;
+    if (tiles >= cu_count && slices >= 32) return 256;
+    if (tiles_half >= cu_count && slices >= 32) return 128;
+    if (tiles128 < 2 * int64_t(cu_count) && 2 * tiles_half >= cu_count && slices >= 64) return 128;
+    if (tiles128 < 2 * int64_t(cu_count) && 4 * tiles >= cu_count && slices >= 128) return 256;
+    return 0;
 }
 
 // offsets: nullptr for the affine mode (a_bstride / b_bstride).
@@ -1345,8 +1358,8 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     // is as fast as NT, and from K = 2048 on the copy no longer pays
     // (8192 x 4096 x 4096: 1886 us with the copy, 1872 without; at K = 1024
     // the copy still wins, 490 against 495).
-    const bool big_nn = (mode == kGemmTiles256 || (mode == kGemmAuto && K >= 2048 &&
-                                                   big_tiles(M, N, K, batch, reduce, d.cu_count, false))) &&
+    const bool big_nn = (mode == kGemmTiles256 || mode == kGemmTiles256x128 ||
+                         (mode == kGemmAuto && K >= 2048 && big_tiles(M, N, K, batch, reduce, d.cu_count, false))) &&
                         std::max(K, N) * BT < (int64_t(1) << 29);
     if (!ta && !tb && batch == 1 && reduce == 1 && !force_simple && M >= kNnViaNtMinRows && N % 4 == 0 &&
         K % 4 == 0 && K <= int64_t(65535) * 64 && aligned16(a) && aligned16(b) && !relu_mask && !big_nn) {
@@ -1392,12 +1405,16 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     } else {
         vec = vec && a_bstride % 4 == 0 && b_bstride % 4 == 0;
     }
-    const int64_t tiles_m256 = (M + BT - 1) / BT, tiles_n256 = (N + BT - 1) / BT;
     const bool big_fits = vec && widest * BT < kMax && reduce == 1 && batch <= 65535 / 32;
-    const bool big = big_fits && (mode == kGemmTiles256 ||
-                                  (automatic && !small && !simple &&
-                                   big_tiles(M, N, K, batch, reduce, d.cu_count, relu_mask != nullptr)));
+    const int big_n = !big_fits                   ? 0
+                      : mode == kGemmTiles256     ? 256
+                      : mode == kGemmTiles256x128 ? 128
+                      : automatic && !small && !simple
+                          ? big_tiles(M, N, K, batch, reduce, d.cu_count, relu_mask != nullptr)
+                          : 0;
+    const bool big = big_n != 0;
     if (big) small = simple = false;
+    const int64_t tiles_m256 = (M + BT - 1) / BT, tiles_n256 = big ? (N + big_n - 1) / big_n : 0;
     const int64_t tiles = big     ? tiles_m256 * tiles_n256
                           : small ? tiles_m32 * tiles_n32
                           : simple ? tiles_m_simple * tiles_n_simple
@@ -1486,10 +1503,10 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
         (bias ? 4.0 * double(N) : 0.0);
     std::optional<Profiled> prof;
     if (!in_caller_scope) prof.emplace(label, flops, bytes);
-    if (ta && tb) launch_variant<true, true>(args, vec, simple, small, big, grid, d.stream);
-    else if (ta) launch_variant<true, false>(args, vec, simple, small, big, grid, d.stream);
-    else if (tb) launch_variant<false, true>(args, vec, simple, small, big, grid, d.stream);
-    else launch_variant<false, false>(args, vec, simple, small, big, grid, d.stream);
+    if (ta && tb) launch_variant<true, true>(args, vec, simple, small, big_n, grid, d.stream);
+    else if (ta) launch_variant<true, false>(args, vec, simple, small, big_n, grid, d.stream);
+    else if (tb) launch_variant<false, true>(args, vec, simple, small, big_n, grid, d.stream);
+    else launch_variant<false, false>(args, vec, simple, small, big_n, grid, d.stream);
     if (splits > 1) {
         after_launch(label);
         const int64_t total = batch * M * N;

@@ -59,7 +59,7 @@ void init_device(Device& d) {
     d.name += std::string(" (") + prop.gcnArchName + ")";
     d.cu_count = prop.multiProcessorCount;
     d.sync_each_launch = env_is("VECTORCORE_HIP_SYNC_EACH", "1");
-    for (int mode : {kGemmSimple, kGemmTiles128, kGemmTiles256})
+    for (int mode : {kGemmSimple, kGemmTiles128, kGemmTiles256, kGemmTiles256x128})
         if (env_is("VECTORCORE_HIP_GEMM", gemm_mode_name(mode))) d.gemm_mode = mode;
     d.ready = true;
 }
@@ -362,6 +362,7 @@ const char* gemm_mode_name(int mode) {
         case kGemmSimple: return "simple";
         case kGemmTiles128: return "mfma128";
         case kGemmTiles256: return "mfma256";
+        case kGemmTiles256x128: return "mfma256x128";
         default: return "mfma";
     }
 }
@@ -544,13 +545,14 @@ const char* vc_hip_gemm_kernel(void) {
 int vc_hip_set_gemm_kernel(const char* name) {
     return guard([&] {
         Device& d = require_device();
-        for (int mode : {kGemmAuto, kGemmSimple, kGemmTiles128, kGemmTiles256})
+        for (int mode : {kGemmAuto, kGemmSimple, kGemmTiles128, kGemmTiles256, kGemmTiles256x128})
             if (name && std::strcmp(name, gemm_mode_name(mode)) == 0) {
                 d.gemm_mode = mode;
                 return;
             }
         fail(VC_HIP_ERR_INVALID_ARGUMENT, std::string("unknown GEMM kernel '") + (name ? name : "(null)") +
-                                              "': expected \"mfma\", \"simple\", \"mfma128\" or \"mfma256\"");
+                                              "': expected \"mfma\", \"simple\", \"mfma128\", \"mfma256\" or "
+                                              "\"mfma256x128\"");
     });
 }
 

@@ -86,9 +86,9 @@ struct Device {
 // ("mfma": the FMA kernel for tiny products, 32 x 32, 128 x 128 or 256 x 256
 // matrix-core tiles by shape), the portable FMA kernel for every product
 // ("simple"), the 128 x 128 tiles for every product ("mfma128"), or the
-// 256 x 256 tiles for every product whose operands allow them, the 128 x 128
-// tiles for the rest ("mfma256").
-enum GemmMode : int { kGemmAuto = 0, kGemmSimple = 1, kGemmTiles128 = 2, kGemmTiles256 = 3 };
+// 256 x 256 ("mfma256") or 256 x 128 ("mfma256x128") tiles for every product
+// whose operands allow them, the 128 x 128 tiles for the rest.
+enum GemmMode : int { kGemmAuto = 0, kGemmSimple = 1, kGemmTiles128 = 2, kGemmTiles256 = 3, kGemmTiles256x128 = 4 };
 const char* gemm_mode_name(int mode);
 
 // Initialises once (thread-safe) and makes the device current on this thread.

@@ -2,7 +2,7 @@
 // wavefront/workgroup double sums with a fixed combine order, the first
 // strict maximum of a row, the one-launch finish (the block that finishes last
 // adds the blocks' partials) and the full sum (fixed chunks, then their sum in
-// a fixed order, in one launch or two).
+// a fixed order, in one launch).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -181,19 +181,24 @@ __device__ inline double chunk_sum(const float* __restrict__ x, int64_t b0, int6
 }
 
 // ---- one launch: the block that finishes last adds the partials -----------
-// Each block writes its partial with a device-scope store, waits for it to
-// complete (s_waitcnt 0: a device-scope store is acknowledged once it is
-// visible at device scope, so no release fence, and no L2 writeback, is
-// needed), then counts itself in on its group's device-scope counter (groups
-// of kDoneGroup blocks, one counter per 128-byte line, so the count is not one
-// long queue on one address). The block that completes a group resets that
-// counter and counts the group in on the top counter; the block that
-// completes the last group reads every partial with device-scope loads and
-// adds them as sum_final_kernel does (thread t takes blocks t, t + 256, ...,
-// then the fixed workgroup tree), so the result does not depend on which
-// block is last, and it resets the top counter for the next launch. Launches
-// on the library's one stream never overlap, so each translation unit's
-// counters (static, zero at load) serve all its one-launch kernels.
+// Only wavefront 0 of a block takes part: the block's other wavefronts leave
+// once its partial is formed, so the CU can start the next block while the
+// count-in's round trips to device scope run. Lane 0 writes the partial with
+// a device-scope store, waits for it to complete (s_waitcnt 0: a device-scope
+// store is acknowledged once it is visible at device scope, so no release
+// fence, and no L2 writeback, is needed), then counts the block in on its
+// group's device-scope counter (groups of kDoneGroup blocks, one counter per
+// 128-byte line, so the count is not one long queue on one address). The
+// block that completes a group resets that counter and counts the group in on
+// the top counter; the block that completes the last group reads every
+// partial with device-scope loads and adds them in one fixed order (lane t
+// takes blocks t, t + 64, ... in ascending order, then the wavefront's fixed
+// butterfly), so the result does not depend on which block is last, and it
+// resets the top counter for the next launch. Launches on the library's one
+// stream never overlap, so each translation unit's counters (static, zero at
+// load) serve all its one-launch kernels; the counter resets need no wait,
+// since nothing later in the same launch reads them and the end of the launch
+// makes them visible to the next.
 
 // The wait that orders a block's partial stores before its counter atomic.
 // The ordering in hardware comes from s_waitcnt 0, which waits until every
@@ -214,64 +219,54 @@ constexpr unsigned kMaxFinishBlocks = kDoneGroup * kDoneGroups;
 static __device__ unsigned int g_group_done[kDoneGroups * kDoneStride];
 static __device__ unsigned int g_groups_done;
 
-// Thread 0 holds the block's partial; every thread of the block learns
-// whether it finished last. Grids of at most kMaxFinishBlocks blocks.
+// Called by the whole of wavefront 0 (and no other wavefront of the block);
+// its lane 0 holds the block's partial. Every lane learns whether the block
+// finished last. Grids of at most kMaxFinishBlocks blocks.
 __device__ inline bool count_in(double block_partial, double* __restrict__ part) {
-    __shared__ int last_block;
+    int last = 0;
     if (threadIdx.x == 0) {
         __hip_atomic_store(&part[blockIdx.x], block_partial, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         wait_stores_visible();
         const unsigned group = blockIdx.x / kDoneGroup, groups = (gridDim.x + kDoneGroup - 1) / kDoneGroup;
         const unsigned members = min(kDoneGroup, gridDim.x - group * kDoneGroup);
         unsigned* counter = &g_group_done[group * kDoneStride];
-        bool last = false;
         if (__hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == members) {
             __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            wait_stores_visible();
             last = __hip_atomic_fetch_add(&g_groups_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == groups;
         }
-        last_block = last;
     }
-    __syncthreads();
-    return last_block;
+    return __builtin_amdgcn_readfirstlane(last) != 0;
 }
 
-// In the block that finished last: the sum of part[0, gridDim.x), valid in
-// thread 0, which also resets the top counter. Device-scope (cache policy
-// sc1 = 16) loads, eight in flight per thread.
-__device__ inline double finish_partials(const double* __restrict__ part, double* lds) {
+// In wavefront 0 of the block that finished last: the sum of
+// part[0, gridDim.x) on every lane, in the order above, with device-scope
+// (cache policy sc1 = 16) loads, sixteen in flight per lane. Also resets the
+// top counter.
+__device__ inline double finish_partials(const double* __restrict__ part) {
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<double*>(part), short(0), int(gridDim.x * sizeof(double)), 0x00020000);
+    const unsigned lane = threadIdx.x;
     double acc = 0.0;
-    for (unsigned b0 = threadIdx.x; b0 < gridDim.x; b0 += 8 * blockDim.x) {
-        double v[8];
+    for (unsigned b0 = lane; b0 < gridDim.x; b0 += 16 * kWave) {
+        double v[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const unsigned b = b0 + u * blockDim.x;  // past the grid: outside the descriptor, reads 0 (not added)
+        for (int u = 0; u < 16; ++u) {
+            const unsigned b = b0 + u * kWave;  // past the grid: outside the descriptor, reads 0 (not added)
             v[u] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rp, b * 8u, 0, 16));
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (b0 + u * blockDim.x < gridDim.x) acc += v[u];
+        for (int u = 0; u < 16; ++u)
+            if (b0 + u * kWave < gridDim.x) acc += v[u];
     }
-    const double total = block_sum(acc, lds);
-    if (threadIdx.x == 0) __hip_atomic_store(&g_groups_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const double total = wave_sum(acc);
+    if (lane == 0) __hip_atomic_store(&g_groups_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return total;
 }
 
-// Stage one: part[b] = sum of x[b*chunk, (b+1)*chunk) in double.
-template <bool Vec>
-__global__ __launch_bounds__(kBlock) void sum_partial_kernel(const float* __restrict__ x, double* __restrict__ part,
-                                                             int64_t n, int64_t chunk) {
-    __shared__ double lds[kBlock / kWave];
-    const int64_t b0 = int64_t(blockIdx.x) * chunk, b1 = b0 + chunk < n ? b0 + chunk : n;
-    const double total = block_sum(chunk_sum<Vec>(x, b0, b1), lds);
-    if (threadIdx.x == 0) part[blockIdx.x] = total;
-}
-
-// Both stages in one launch (grids of at most kMaxFinishBlocks chunks, and at
-// least one block: an empty input sums to 0): the same partials, added in the
-// same order as sum_final_kernel, by the block that finishes last.
+// The full sum in one launch (grids of at most kMaxFinishBlocks chunks, and
+// at least one block: an empty input sums to 0): block b adds
+// x[b*chunk, (b+1)*chunk) in double (chunk_sum, then the workgroup tree), and
+// the block that finishes last adds the blocks' partials.
 template <bool Vec, class Finish>
 __global__ __launch_bounds__(kBlock) void sum_finish_kernel(const float* __restrict__ x, double* __restrict__ part,
                                                             float* __restrict__ out, int64_t n, int64_t chunk,
@@ -279,30 +274,9 @@ __global__ __launch_bounds__(kBlock) void sum_finish_kernel(const float* __restr
     __shared__ double lds[kBlock / kWave];
     const int64_t b0 = int64_t(blockIdx.x) * chunk, b1 = b0 + chunk < n ? b0 + chunk : n;
     const double partial = block_sum(chunk_sum<Vec>(x, b0, b1), lds);
+    if (threadIdx.x >= kWave) return;  // wavefront 0 counts the block in
     if (!count_in(partial, part)) return;
-    const double total = finish_partials(part, lds);
-    if (threadIdx.x == 0) out[0] = finish(float(total));
-}
-
-// Stage two: out = finish(float(sum of the partials)); thread t takes
-// b = t, t + blockDim, ... (eight loads in flight), then the fixed workgroup
-// tree.
-template <class Finish>
-__global__ __launch_bounds__(kBlock) void sum_final_kernel(const double* __restrict__ part, float* __restrict__ out,
-                                                           int64_t blocks, Finish finish) {
-    __shared__ double lds[kBlock / kWave];
-    double acc = 0.0;
-    const int64_t step = blockDim.x;
-    int64_t b = threadIdx.x;
-    for (; b + 7 * step < blocks; b += 8 * step) {
-        double v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = part[b + u * step];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc += v[u];
-    }
-    for (; b < blocks; b += step) acc += part[b];
-    const double total = block_sum(acc, lds);
+    const double total = finish_partials(part);
     if (threadIdx.x == 0) out[0] = finish(float(total));
 }
 

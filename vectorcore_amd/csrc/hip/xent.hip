@@ -306,14 +306,13 @@ __device__ inline void load_row(f4 (&v)[NV], const float* __restrict__ row, int6
 }
 
 // Rows held in registers. Each wavefront walks rows r, r + W, ... (W
-// wavefronts in the grid) and loads its next row (and target) before working
-// on the current one, so memory latency overlaps the exp work of the row
-// before. The loss terms are summed on the way: each wavefront in row order,
-// then the block's wavefronts in order, into one double per block.
+// wavefronts in the grid); the other wavefronts in flight on the SIMD hide a
+// row's load latency. The loss terms are summed on the way: each wavefront in
+// row order, then the block's wavefronts in order, into one double per block.
 //
 // The block that finishes last also finishes the loss, so the forward is one
 // launch (red::count_in and red::finish_partials: the partials are added in
-// block order whichever block is last).
+// one fixed order whichever block is last).
 
 // ---- two rows per wavefront: lanes 0-31 hold one row, lanes 32-63 the next --
 // For rows of at most 1024 classes. A row's cross-lane reductions then take
@@ -488,21 +487,22 @@ struct NegateDivide {
 };
 
 // The end of a one-launch forward: each wavefront's loss terms are in
-// wave_terms. Block b adds them in wave order into its partial; the block
-// that finishes last adds all partials in block order (red::count_in,
-// red::finish_partials) and writes the loss.
+// wave_terms. Wavefront 0 adds them in wave order into the block's partial
+// (the block's other wavefronts leave); the block that finishes last adds all
+// partials in red::finish_partials' order (red::count_in) and writes the loss.
 // With host_loss (pinned host memory), the loss is also written there, for a
 // reader that waits for this kernel's completion only.
 __device__ inline void finish_loss(double* wave_terms, double* __restrict__ part, int64_t rows,
                                    float* __restrict__ loss, float* __restrict__ host_loss) {
     __syncthreads();
+    if (threadIdx.x >= kWave) return;
     double sum = 0.0;
     if (threadIdx.x == 0) {
         sum = wave_terms[0];
         for (int w = 1; w < kRowsPerBlock; ++w) sum += wave_terms[w];
     }
     if (!red::count_in(sum, part)) return;
-    const double total = red::finish_partials(part, wave_terms);
+    const double total = red::finish_partials(part);
     if (threadIdx.x == 0) {
         const float value = NegateDivide{float(rows)}(float(total));
         loss[0] = value;
@@ -780,10 +780,11 @@ int64_t cached_resident_blocks() {
 
 // The forward. With `publish`, the loss is also copied into that mirror's
 // host slot: by the finishing block of a register-held row kernel, whose
-// dispatch then carries the mirror's completion event, or, when the profiler
-// holds the dispatch's events or the rows are streamed, by a copy launched
-// after the forward. With row_argmax, every path also writes each row's
-// argmax (as a float index) from the row it already holds.
+// dispatch then carries the mirror's completion event (recorded on the stream
+// right after the dispatch when the profiler holds the dispatch's events), or,
+// when the rows are streamed, by a copy launched after the forward. With
+// row_argmax, every path also writes each row's argmax (as a float index)
+// from the row it already holds.
 void xent_forward(const float* logits, const int32_t* targets, size_t rows, size_t classes, float* row_stats,
                   float* loss, float* row_argmax, vc_hip_mirror* publish) {
     Device& d = require_device();
@@ -818,13 +819,15 @@ void xent_forward(const float* logits, const int32_t* targets, size_t rows, size
     Scratch part(size_t(std::max<int64_t>(row_blocks, (R + red::sum_chunk(R) - 1) / red::sum_chunk(R))) *
                  sizeof(double));
     // Register-held rows (nv <= 16) write the loss's host copy from their
-    // finishing block, the dispatch signalling the mirror, unless the
-    // profiler holds the dispatch's events.
+    // finishing block, the dispatch signalling the mirror; when the profiler
+    // holds the dispatch's events, the mirror's event is recorded after it.
     float* host_loss = nullptr;
     hipEvent_t published = nullptr;
-    if (publish && nv <= 16 && !p.stop_event()) {
+    bool record_published = false;
+    if (publish && nv <= 16) {
         host_loss = publish->host;
-        published = publish->done;
+        if (p.stop_event()) record_published = true;
+        else published = publish->done;
     }
     auto row_launch = [&](auto kernel, unsigned blocks) {
         if (published)
@@ -862,6 +865,11 @@ void xent_forward(const float* logits, const int32_t* targets, size_t rows, size
 #undef VC_XENT_ROWS
     }
     after_launch("xent_forward");
+    if (record_published) {
+        const hipError_t e = hipEventRecord(publish->done, d.stream);
+        if (e != hipSuccess)
+            fail(VC_HIP_ERR_RUNTIME, std::string("xent_forward: event record failed: ") + hipGetErrorString(e));
+    }
     if (publish && !host_loss) launch_mirror(publish, loss);
     p.done();
 }

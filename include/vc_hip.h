@@ -302,6 +302,30 @@ int vc_hip_matmul_relu_mask_colsum_pending(const float* a, const float* b, float
  * runtime finds those ops applied to a product not yet computed. */
 int vc_hip_matmul_bias_relu(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
                             const float* bias, int relu);
+/* ReLU bitmask of an m x n matrix: bit i % 32 of word relu_bits[(i / 32) * n + j]
+ * stands for element (i, j); ceil(m / 32) * n words. */
+/* vc_hip_matmul_bias_relu with relu on, which also writes the ReLU bitmask
+ * of [c > 0] when the product runs on the kernel that can (the 256-row
+ * tiles, chosen by size): *bits_written is then 1, otherwise 0 and relu_bits
+ * is not written. c is the same bits either way. No counterpart in the
+ * reference: the bits stand for the mask that the ReLU's backward rule
+ * (src/ops.cpp:395-403) reads from the layer's output, so that the product
+ * giving the ReLU's upstream gradient reads 1 bit per element instead of 32
+ * (vc_hip_matmul_relu_bits). */
+int vc_hip_matmul_bias_relu_bits(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                                 const float* bias, uint32_t* relu_bits, int* bits_written);
+/* vc_hip_matmul_relu_mask for one product (batch 1), the mask given as a ReLU
+ * bitmask (mask[i][j] > 0 exactly where its bit is set): the same bits as
+ * vc_hip_matmul_relu_mask with that mask. No counterpart in the reference:
+ * the fused ReLU backward of vc_hip_matmul_relu_mask (src/ops.cpp:395-403). */
+int vc_hip_matmul_relu_bits(const float* a, const float* b, float* c, size_t m, size_t k, size_t n, int trans_a,
+                            int trans_b, const uint32_t* relu_bits);
+/* vc_hip_matmul_relu_mask_colsum_pending with the mask given as a ReLU
+ * bitmask: the same bits (c, the column sums, the handle's) as with the float
+ * mask it stands for. Serves the same rules. */
+int vc_hip_matmul_relu_bits_colsum_pending(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                                           int trans_a, int trans_b, const uint32_t* relu_bits, float* column_sum,
+                                           vc_hip_colsum** pending);
 
 /* Batch-reduced product for gradients of a batch-broadcast operand
  * (src/ops.cpp:252-260 followed by sum_to_shape over the batch):

@@ -110,6 +110,10 @@ _SIGNATURES = {
     "vc_hip_matmul_relu_mask_colsum_pending": ([_vp, _vp, _vp, _sz, _sz, _sz, _i, _i, _vp, _vp,
                                                 ctypes.POINTER(_vp)], _i),
     "vc_hip_matmul_bias_relu": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp, _i], _i),
+    "vc_hip_matmul_bias_relu_bits": ([_vp, _vp, _vp, _sz, _sz, _sz, _vp, _vp, ctypes.POINTER(_i)], _i),
+    "vc_hip_matmul_relu_bits": ([_vp, _vp, _vp, _sz, _sz, _sz, _i, _i, _vp], _i),
+    "vc_hip_matmul_relu_bits_colsum_pending": ([_vp, _vp, _vp, _sz, _sz, _sz, _i, _i, _vp, _vp,
+                                                ctypes.POINTER(_vp)], _i),
     "vc_hip_matmul_reduce": ([_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _sz, _i, _i], _i),
     "vc_hip_transpose_last2": ([_vp, _vp, _sz, _sz, _sz], _i),
     "vc_hip_reduce_sum": ([_vp, _sz, _vp], _i),

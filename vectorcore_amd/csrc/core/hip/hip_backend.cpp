@@ -135,10 +135,26 @@ public:
         }
         if (deferred_) {
             const DeferredProduct& d = *deferred_;
-            check(vc_hip_matmul_bias_relu(d.a->ptr() + d.a_offset, d.b->ptr() + d.b_offset, static_cast<float*>(ptr_),
-                                          d.m, d.k, d.n, d.bias ? d.bias->ptr() + d.bias_offset : nullptr,
-                                          d.relu ? 1 : 0),
-                  "HIP matmul failed");
+            const float* bias = d.bias ? d.bias->ptr() + d.bias_offset : nullptr;
+            if (d.relu) {
+                // With the layer's ReLU bitmask where its kernel writes one,
+                // for the product that applies the ReLU's backward rule.
+                auto bits = std::make_shared<HipStorage>((d.m + 31) / 32 * d.n);
+                int written = 0;
+                check(vc_hip_matmul_bias_relu_bits(d.a->ptr() + d.a_offset, d.b->ptr() + d.b_offset,
+                                                   static_cast<float*>(ptr_), d.m, d.k, d.n, bias,
+                                                   reinterpret_cast<uint32_t*>(bits->ptr()), &written),
+                      "HIP matmul failed");
+                if (written) {
+                    relu_bits_ = std::move(bits);
+                    relu_bits_rows_ = d.m;
+                    relu_bits_cols_ = d.n;
+                }
+            } else {
+                check(vc_hip_matmul_bias_relu(d.a->ptr() + d.a_offset, d.b->ptr() + d.b_offset,
+                                              static_cast<float*>(ptr_), d.m, d.k, d.n, bias, 0),
+                      "HIP matmul failed");
+            }
             deferred_.reset();  // drops the operands
         }
         return static_cast<float*>(ptr_);
@@ -232,6 +248,16 @@ public:
         return std::move(row_argmax_);
     }
 
+    // The ReLU bitmask ([value > 0], in vc_hip_matmul_bias_relu_bits' layout)
+    // of this storage's contents as [rows, cols], written by the fused layer
+    // product that computed them. Kept until the storage is written in place.
+    const uint32_t* relu_bits(std::size_t rows, std::size_t cols) const {
+        std::lock_guard<std::recursive_mutex> lock(state_mutex());
+        if (!relu_bits_ || rows != relu_bits_rows_ || cols != relu_bits_cols_ || rows * cols != elements_)
+            return nullptr;
+        return reinterpret_cast<const uint32_t*>(relu_bits_->ptr());
+    }
+
     // The deferred product this storage still has to compute, if any (a copy
     // for building a product with a longer epilogue).
     std::optional<DeferredProduct> pending() const {
@@ -278,6 +304,7 @@ public:
         shadow_valid_ = false;
         column_sum_.reset();  // about to be stale
         row_argmax_.reset();
+        relu_bits_.reset();
         if (mirror_) {  // the published value is about to be stale
             (void)vc_hip_mirror_release(mirror_);
             mirror_ = nullptr;
@@ -333,6 +360,8 @@ private:
     std::size_t column_sum_rows_ = 0, column_sum_cols_ = 0;
     mutable std::shared_ptr<HipStorage> row_argmax_;  // see set_row_argmax
     mutable std::size_t row_argmax_offset_ = 0, row_argmax_rows_ = 0, row_argmax_cols_ = 0;
+    mutable std::shared_ptr<HipStorage> relu_bits_;  // see relu_bits
+    mutable std::size_t relu_bits_rows_ = 0, relu_bits_cols_ = 0;
     bool shadow_valid_;
 };
 
@@ -821,15 +850,31 @@ std::shared_ptr<Storage> HipBackend::matmul_relu_mask(const Storage& a, std::siz
         check(vc_hip_fill(out->ptr(), batch * m * n, 0.0F), "HIP fill failed");
         return out;
     }
-    if (column_sum && batch == 1 && a_offsets[0] == 0 && b_offsets[0] == 0) {
+    // The mask as the ReLU bitmask its producer kept, when it is the whole
+    // storage of a layer's fused product: the same bits, 1/32 of the reads.
+    const bool single = batch == 1 && a_offsets[0] == 0 && b_offsets[0] == 0;
+    const uint32_t* bits = single && mask_offset == 0 ? as_hip(mask).relu_bits(m, n) : nullptr;
+    if (column_sum && single) {
         auto sums = fresh(n);
         vc_hip_colsum* pending = nullptr;
-        check(vc_hip_matmul_relu_mask_colsum_pending(dptr(a, a_offset), dptr(b, b_offset), out->ptr(), m, k, n,
-                                                     trans_a ? 1 : 0, trans_b ? 1 : 0, dptr(mask, mask_offset),
-                                                     sums->ptr(), &pending),
-              "HIP matmul failed");
+        if (bits)
+            check(vc_hip_matmul_relu_bits_colsum_pending(dptr(a, a_offset), dptr(b, b_offset), out->ptr(), m, k, n,
+                                                         trans_a ? 1 : 0, trans_b ? 1 : 0, bits, sums->ptr(),
+                                                         &pending),
+                  "HIP matmul failed");
+        else
+            check(vc_hip_matmul_relu_mask_colsum_pending(dptr(a, a_offset), dptr(b, b_offset), out->ptr(), m, k, n,
+                                                         trans_a ? 1 : 0, trans_b ? 1 : 0, dptr(mask, mask_offset),
+                                                         sums->ptr(), &pending),
+                  "HIP matmul failed");
         if (pending) sums->set_pending_sums(pending);
         out->set_column_sum(std::move(sums), m, n);
+        return out;
+    }
+    if (bits) {
+        check(vc_hip_matmul_relu_bits(dptr(a, a_offset), dptr(b, b_offset), out->ptr(), m, k, n, trans_a ? 1 : 0,
+                                      trans_b ? 1 : 0, bits),
+              "HIP matmul failed");
         return out;
     }
     check(vc_hip_matmul_relu_mask(dptr(a, a_offset), dptr(b, b_offset), out->ptr(), m, k, n, a_offsets.data(),

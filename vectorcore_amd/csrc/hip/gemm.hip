@@ -91,6 +91,10 @@ struct GemmArgs {
     double* col_part;              // null, or partial rows of C's column sums (batch 1, no split), in
                                    //   double: MFMA kernel 2 tiles_m rows (one per 64 rows of a tile),
                                    //   FMA kernel tiles_m rows (one per 16-row tile)
+    // ReLU bitmasks (gemm_big_kernel with A k-contiguous, batch 1, no split):
+    // bit r % 32 of word (r / 32) N + c stands for element (r, c).
+    const uint32_t* relu_bits;     // null, or the fused ReLU backward's mask as such bits: C *= [bit]
+    uint32_t* relu_bits_out;       // null, or receives the bits of [C > 0] after the forward epilogue
 };
 
 // The forward epilogue, in the order of the unfused ops: the row-broadcast add
@@ -720,6 +724,30 @@ __device__ inline void big_epilogue(const GemmArgs& p, f16v (&acc)[2][2], const 
                     acc[i][j][v] = value * (xv > 0.0f ? 1.0f : 0.0f);
                 }
     }
+    // A lane's 16 values of a 32-row group of one column (rows as bc.row
+    // with A k-contiguous) are bits 4 (lane / 32) + 8 (v / 4) + v % 4 of that
+    // column's word for the group; rows wm + 32 i .. of the tile are group
+    // (m0 + wm) / 32 + i.
+    const int bit_base = 4 * (lane >> 5);
+    if (AKC && p.relu_bits && p.splits == 1) {
+        const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.relu_bits + int64_t((m0 + wm) / 32) * p.N + n0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = bc.col(j);
+                const bool ok = wm + 32 * i < row_lim && col < col_lim;
+                const uint32_t word =
+                    __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? uint32_t(i * p.N + col) * 4u : kOutOfRange, 0, 0) >>
+                    bit_base;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const float keep = float((word >> (8 * (v >> 2) + (v & 3))) & 1u);
+                    const float value = acc[i][j][v];
+                    acc[i][j][v] = value * keep;
+                }
+            }
+    }
     if (p.splits == 1 && (p.bias || p.relu)) {
         float bias[2] = {0.0f, 0.0f};
         if (p.bias) {
@@ -731,15 +759,42 @@ __device__ inline void big_epilogue(const GemmArgs& p, f16v (&acc)[2][2], const 
                     float, __builtin_amdgcn_raw_buffer_load_b32(rb, col < col_lim ? uint32_t(col) * 4u : kOutOfRange, 0, 0));
             }
         }
+        if (AKC && p.relu_bits_out && p.relu) {
+            // bias_relu with the ReLU bitmask of its results: the compare that
+            // picks a value also sets its bit. Each half-wave holds half of a
+            // column's 32 rows: the two halves' bits are joined, and lanes
+            // 0-31 write the words of their columns.
+            const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.relu_bits_out + int64_t((m0 + wm) / 32) * p.N + n0);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < 2; ++j) {
+                    uint32_t bits = 0;
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const float value = acc[i][j][v];
-                    acc[i][j][v] = bias_relu(value, bias[j], p.relu != 0);
+                    for (int v = 0; v < 16; ++v) {
+                        const float value = acc[i][j][v] + bias[j];
+                        const bool positive = value > 0.0f;
+                        acc[i][j][v] = positive ? value : 0.0f;
+                        bits |= positive ? 1u << (8 * (v >> 2) + (v & 3)) : 0u;
+                    }
+                    bits <<= bit_base;
+                    bits |= uint32_t(__shfl_xor(int(bits), 32, 64));
+                    const int col = bc.col(j);
+                    const bool ok = lane < 32 && wm + 32 * i < row_lim && col < col_lim;
+                    __builtin_amdgcn_raw_buffer_store_b32(bits, rw, ok ? uint32_t(i * p.N + col) * 4u : kOutOfRange, 0,
+                                                          0);
                 }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const float value = acc[i][j][v];
+                        acc[i][j][v] = bias_relu(value, bias[j], p.relu != 0);
+                    }
+        }
     }
     // Partial rows past the 2 ceil(M / 128) that the 128 x 128 tiles write
     // (and the caller allocates) lie wholly below C and are not written.
@@ -971,6 +1026,18 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
         if (relu_mask) acc = acc * (relu_mask[t] > 0.0f ? 1.0f : 0.0f);
         if (bias || relu) acc = bias_relu(acc, bias ? bias[i % n] : 0.0f, relu != 0);
         c[t] = acc;
+    }
+}
+
+// The float mask [bit] of a ReLU bitmask (bit r % 32 of word (r / 32) n + c
+// for element (r, c)), for a product that does not take gemm_big_kernel.
+__global__ __launch_bounds__(256) void relu_bits_expand_kernel(const uint32_t* __restrict__ bits,
+                                                               float* __restrict__ mask, int64_t m, int64_t n) {
+    const int64_t total = m * n;
+    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+        const int64_t r = t / n, col = t % n;
+        mask[t] = float((bits[(r / 32) * n + col] >> (r % 32)) & 1u);
     }
 }
 
@@ -1339,10 +1406,13 @@ int big_tiles(int64_t M, int64_t N, int64_t K, int64_t batch, int64_t reduce, in
 void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_t K, int64_t batch, int64_t a_bstride,
           int64_t b_bstride, const std::vector<int64_t>* offsets, int64_t reduce, int64_t a_rstride, int64_t b_rstride,
           bool ta, bool tb, const float* relu_mask = nullptr, const float* bias = nullptr, bool relu = false,
-          bool in_caller_scope = false, float* column_sum = nullptr, vc_hip_colsum** pending = nullptr) {
+          bool in_caller_scope = false, float* column_sum = nullptr, vc_hip_colsum** pending = nullptr,
+          const uint32_t* relu_bits = nullptr, uint32_t* relu_bits_out = nullptr, bool* bits_written = nullptr) {
     Device& d = require_device();
     if (M < 0 || N < 0 || K < 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "negative matrix dimension");
     if (pending) *pending = nullptr;
+    if (bits_written) *bits_written = false;
+    if (relu_mask && relu_bits) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul: a ReLU mask and ReLU bits at once");
     if (column_sum && (batch != 1 || reduce != 1))
         fail(VC_HIP_ERR_INVALID_ARGUMENT, "a fused column sum needs a single product");
     if (pending && !column_sum) fail(VC_HIP_ERR_INVALID_ARGUMENT, "pending column sums need a column-sum buffer");
@@ -1362,7 +1432,8 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
                          (mode == kGemmAuto && K >= 2048 && big_tiles(M, N, K, batch, reduce, d.cu_count, false))) &&
                         std::max(K, N) * BT < (int64_t(1) << 29);
     if (!ta && !tb && batch == 1 && reduce == 1 && !force_simple && M >= kNnViaNtMinRows && N % 4 == 0 &&
-        K % 4 == 0 && K <= int64_t(65535) * 64 && aligned16(a) && aligned16(b) && !relu_mask && !big_nn) {
+        K % 4 == 0 && K <= int64_t(65535) * 64 && aligned16(a) && aligned16(b) && !relu_mask && !relu_bits &&
+        !big_nn) {
         Profiled prof("gemm_nn", 2.0 * double(M) * double(N) * double(K),
                       4.0 * double(M * K + 2 * K * N + M * N) + (bias ? 4.0 * double(N) : 0.0));
         Scratch bt(size_t(K * N) * sizeof(float));
@@ -1371,7 +1442,7 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
         after_launch("gemm_nn");
         // Inside this scope: the transpose and the product are timed together.
         gemm(a, bt.as<float>(), c, M, N, K, 1, 0, 0, nullptr, 1, 0, 0, false, true, nullptr, bias, relu, true,
-             column_sum, pending);
+             column_sum, pending, nullptr, relu_bits_out, bits_written);
         prof.done();
         return;
     }
@@ -1487,7 +1558,21 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     const dim3 grid(unsigned(tiles), unsigned(std::min<int64_t>(batch * splits, 65535)));
     const char* label = variant_label(ta, tb);
     const double flops = 2.0 * double(M) * double(N) * double(K) * double(batch) * double(reduce);
+    // ReLU bitmasks go with gemm_big_kernel's epilogue for one product with A
+    // k-contiguous and no split. Elsewhere a consumer's bits are expanded into
+    // a float mask first (below), and a producer writes none.
+    const bool bits_here = big && !ta && batch == 1 && reduce == 1 && splits == 1;
+    Scratch expanded(relu_bits && !bits_here ? size_t(M * N) * sizeof(float) : 4);
+    const uint32_t* expand_from = nullptr;
+    if (relu_bits && !bits_here) {
+        expand_from = relu_bits;
+        relu_bits = nullptr;
+        relu_mask = expanded.as<float>();
+    }
     args.relu_mask = relu_mask;
+    args.relu_bits = relu_bits;
+    args.relu_bits_out = bits_here && relu && relu_bits_out ? relu_bits_out : nullptr;
+    if (bits_written) *bits_written = args.relu_bits_out != nullptr;
     args.bias = bias;
     args.relu = relu ? 1 : 0;
     // The column sums of C (a bias gradient) come from partial rows that the
@@ -1500,9 +1585,14 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     if (sums) args.col_part = sums->part;
     const double bytes =
         4.0 * (double(M * K + K * N) * double(reduce) + double(M * N) * (relu_mask ? 2.0 : 1.0)) * double(batch) +
-        (bias ? 4.0 * double(N) : 0.0);
+        (bias ? 4.0 * double(N) : 0.0) + (relu_bits || args.relu_bits_out ? double(M * N) / 8.0 : 0.0);
     std::optional<Profiled> prof;
     if (!in_caller_scope) prof.emplace(label, flops, bytes);
+    if (expand_from) {
+        launch(relu_bits_expand_kernel, dim3(unsigned(std::min<int64_t>((M * N + 255) / 256, int64_t(d.cu_count) * 16))),
+               dim3(256), 0, d.stream, expand_from, expanded.as<float>(), M, N);
+        after_launch("relu_bits_expand");
+    }
     if (ta && tb) launch_variant<true, true>(args, vec, simple, small, big_n, grid, d.stream);
     else if (ta) launch_variant<true, false>(args, vec, simple, small, big_n, grid, d.stream);
     else if (tb) launch_variant<false, true>(args, vec, simple, small, big_n, grid, d.stream);
@@ -1575,9 +1665,11 @@ int vc_hip_matmul_relu_mask(const float* a, const float* b, float* c, size_t m, 
 
 namespace {
 void relu_mask_colsum(const float* a, const float* b, float* c, size_t m, size_t k, size_t n, int trans_a,
-                      int trans_b, const float* mask, float* column_sum, vc_hip_colsum** pending) {
+                      int trans_b, const float* mask, float* column_sum, vc_hip_colsum** pending,
+                      const uint32_t* bits = nullptr) {
     if (pending) *pending = nullptr;
-    if (!mask || !column_sum) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask_colsum: null mask or column sum");
+    if ((!mask && !bits) || !column_sum)
+        fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask_colsum: null mask or column sum");
     if (n == 0) return;
     if (m == 0) {  // an empty column sum is zero
         const int rc = vc_hip_fill(column_sum, n, 0.0f);
@@ -1586,7 +1678,7 @@ void relu_mask_colsum(const float* a, const float* b, float* c, size_t m, size_t
     }
     if (k == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_mask_colsum needs k > 0");
     gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), 1, 0, 0, nullptr, 1, 0, 0, trans_a != 0, trans_b != 0, mask,
-         nullptr, false, false, column_sum, pending);
+         nullptr, false, false, column_sum, pending, bits);
 }
 }  // namespace
 
@@ -1613,6 +1705,39 @@ int vc_hip_matmul_bias_relu(const float* a, const float* b, float* c, size_t m, 
         if (k == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_bias_relu needs k > 0");
         gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), 1, 0, 0, nullptr, 1, 0, 0, false, false, nullptr, bias,
              relu != 0);
+    });
+}
+
+int vc_hip_matmul_bias_relu_bits(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                                 const float* bias, uint32_t* relu_bits, int* bits_written) {
+    return guard([&] {
+        if (!relu_bits || !bits_written) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_bias_relu_bits: null bits or flag");
+        *bits_written = 0;
+        if (m == 0 || n == 0) return;
+        if (k == 0) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_bias_relu_bits needs k > 0");
+        bool written = false;
+        gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), 1, 0, 0, nullptr, 1, 0, 0, false, false, nullptr, bias, true,
+             false, nullptr, nullptr, nullptr, relu_bits, &written);
+        *bits_written = written ? 1 : 0;
+    });
+}
+
+int vc_hip_matmul_relu_bits(const float* a, const float* b, float* c, size_t m, size_t k, size_t n, int trans_a,
+                            int trans_b, const uint32_t* relu_bits) {
+    return guard([&] {
+        if (!relu_bits) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_bits: null bits");
+        gemm(a, b, c, int64_t(m), int64_t(n), int64_t(k), 1, 0, 0, nullptr, 1, 0, 0, trans_a != 0, trans_b != 0,
+             nullptr, nullptr, false, false, nullptr, nullptr, relu_bits);
+    });
+}
+
+int vc_hip_matmul_relu_bits_colsum_pending(const float* a, const float* b, float* c, size_t m, size_t k, size_t n,
+                                           int trans_a, int trans_b, const uint32_t* relu_bits, float* column_sum,
+                                           vc_hip_colsum** pending) {
+    return guard([&] {
+        if (!pending) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_bits_colsum_pending: null handle pointer");
+        if (!relu_bits) fail(VC_HIP_ERR_INVALID_ARGUMENT, "matmul_relu_bits_colsum_pending: null bits");
+        relu_mask_colsum(a, b, c, m, k, n, trans_a, trans_b, nullptr, column_sum, pending, relu_bits);
     });
 }
 

@@ -1385,10 +1385,12 @@ bool small_tiles(int64_t K, int64_t products, int64_t tiles128, bool tiny, bool 
 //   CU): 256 x 128 tiles split in two (4096 x 1000 x 8192 TN 504 -> 469,
 //   1024 x 4096 x 8192 TN 504 -> 469; 256 x 256 tiles split in four took
 //   482 and 485), or 256 x 256 tiles split in four.
-// A fused ReLU mask adds its loads to the epilogue, which with one workgroup
-// per CU nothing overlaps and every CU reaches at once: masked products need 64
-// slices (8192 x 4096 x 4096 masked NT 1915 -> 1846 us; 8192 x 4096 x 1000
-// 508 -> 518, so it stays).
+// A fused float ReLU mask adds its loads to the epilogue, which with one
+// workgroup per CU nothing overlaps and every CU reaches at once: masked
+// products need 64 slices (8192 x 4096 x 4096 masked NT 1915 -> 1846 us;
+// 8192 x 4096 x 1000 508 -> 518, so it stays). A mask given as ReLU bits (one
+// load per 32 values) takes the unmasked rule (8192 x 4096 x 1000: 512 us on
+// the 128 x 128 tiles with the float mask, 487 on the 256 x 256 with the bits).
 int big_tiles(int64_t M, int64_t N, int64_t K, int64_t batch, int64_t reduce, int cu_count, bool masked) {
     const int64_t tiles = ((M + BT - 1) / BT) * ((N + BT - 1) / BT) * batch;
     const int64_t tiles_half = ((M + BT - 1) / BT) * ((N + 127) / 128) * batch;

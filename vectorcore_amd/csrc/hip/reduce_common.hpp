@@ -240,22 +240,23 @@ __device__ inline bool count_in(double block_partial, double* __restrict__ part)
 
 // In wavefront 0 of the block that finished last: the sum of
 // part[0, gridDim.x) on every lane, in the order above, with device-scope
-// (cache policy sc1 = 16) loads, sixteen in flight per lane. Also resets the
-// top counter.
+// (cache policy sc1 = 16) loads, 32 in flight per lane (one round for up to
+// 2048 blocks: 16 measured ~1% slower on a 2048-block forward). Also resets
+// the top counter.
 __device__ inline double finish_partials(const double* __restrict__ part) {
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<double*>(part), short(0), int(gridDim.x * sizeof(double)), 0x00020000);
     const unsigned lane = threadIdx.x;
     double acc = 0.0;
-    for (unsigned b0 = lane; b0 < gridDim.x; b0 += 16 * kWave) {
-        double v[16];
+    for (unsigned b0 = lane; b0 < gridDim.x; b0 += 32 * kWave) {
+        double v[32];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
+        for (int u = 0; u < 32; ++u) {
             const unsigned b = b0 + u * kWave;  // past the grid: outside the descriptor, reads 0 (not added)
             v[u] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rp, b * 8u, 0, 16));
         }
 #pragma unroll
-        for (int u = 0; u < 16; ++u)
+        for (int u = 0; u < 32; ++u)
             if (b0 + u * kWave < gridDim.x) acc += v[u];
     }
     const double total = wave_sum(acc);

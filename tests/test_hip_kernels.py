@@ -305,6 +305,40 @@ def test_gemm_batch_reduce_matches_summed_products(gemm_kernel):
     np.testing.assert_allclose(out.numpy(), expected, rtol=1e-4, atol=1e-4 * np.sqrt(3 * 96))
 
 
+# Config 2's broadcast dB (8 products of 1024^3: one product per split on
+# 256 x 128 tiles), partial tiles with 3 products, K past the last slice, all
+# four transposes, and a product count that exceeds one round (the 128 x 128
+# tiles then, whatever the setting).
+@pytest.mark.parametrize("m,k,n,count", [(1024, 1024, 1024, 8), (300, 100, 520, 3), (1030, 64, 700, 2),
+                                         (2048, 256, 2048, 8)])
+def test_batch_reduce_on_the_256_row_tiles_gives_the_bits_of_the_128_tiles(m, k, n, count):
+    """A batch reduction split one product per split computes each product's
+    64 x 64 blocks as the 128 x 128 tiles do and adds the partials in split
+    order: the same bits on both tile sizes."""
+    rng = np.random.default_rng(m + k + n + count)
+    for ta, tb in ((1, 0), (0, 1), (0, 0), (1, 1)):
+        a = rng.standard_normal((count, k, m) if ta else (count, m, k)).astype(np.float32)
+        b = rng.standard_normal((count, n, k) if tb else (count, k, n)).astype(np.float32)
+        da, db = C.Buffer.of(a), C.Buffer.of(b)
+        outs = {}
+        for kernel in ("mfma128", "mfma", "mfma256x128", "mfma256"):
+            with C.gemm_kernel(kernel):
+                out = C.Buffer((m, n))
+                C.check(C.lib().vc_hip_matmul_reduce(da.ptr, db.ptr, out.ptr, m, k, n, count, m * k, k * n, ta, tb))
+                outs[kernel] = out.numpy()
+        # The automatic setting takes the 256 x 128 tiles for config 2's case;
+        # the smaller products take the 32 x 32 tiles (other bits).
+        same = ("mfma", "mfma256x128", "mfma256") if (m, k, n, count) == (1024, 1024, 1024, 8) else \
+            ("mfma256x128", "mfma256")
+        for kernel in same:
+            np.testing.assert_array_equal(outs[kernel], outs["mfma128"], err_msg=f"{kernel} ta={ta} tb={tb}")
+        rows = rng.choice(m, min(m, 24), replace=False)
+        opa = np.swapaxes(a, 1, 2) if ta else a
+        opb = np.swapaxes(b, 1, 2) if tb else b
+        want = np.einsum("zik,zkj->ij", opa[:, rows].astype(np.float64), opb.astype(np.float64))
+        np.testing.assert_allclose(outs["mfma"][rows], want, rtol=1e-4, atol=1e-4 * np.sqrt(count * k))
+
+
 def binary_dev(a, b, op):
     a, b = K.f32(a), K.f32(b)
     shape = K.broadcast_shape(a.shape, b.shape)

@@ -860,17 +860,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_big_kernel(GemmArgs p) {
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
     const int wm = (wave >> 1) * 128, wn = (wave & 1) * (BN_ / 2);
     const int kt_total = (p.K + BK - 1) / BK;
-    // One job (output matrix, or split of one) per workgroup row of the grid,
-    // and no batch reduction: loops around the K loop here would make the
-    // register allocator spill.
+    // One job (output matrix, or split of one) per workgroup row of the grid:
+    // loops around the K loop here would make the register allocator spill.
+    // A batch reduction is split one product per split (the host sees to
+    // it), which the 128 x 128 tiles do too when they split one: split s
+    // multiplies product s over the whole K.
     {
         const int64_t job = blockIdx.y;
         const int64_t z = uniform64(job / p.splits);
         const int split = __builtin_amdgcn_readfirstlane(int(job - z * p.splits));
-        const int kt_begin = split * p.kt_per_split;
-        const int kt_end = min(kt_total, kt_begin + p.kt_per_split);
-        const int64_t aoff = uniform64(p.table ? p.table[2 * z] : z * p.a_bstride);
-        const int64_t boff = uniform64(p.table ? p.table[2 * z + 1] : z * p.b_bstride);
+        const bool per_product = p.reduce > 1;
+        const int kt_begin = per_product ? 0 : split * p.kt_per_split;
+        const int kt_end = per_product ? kt_total : min(kt_total, kt_begin + p.kt_per_split);
+        const int64_t aoff = uniform64((p.table ? p.table[2 * z] : z * p.a_bstride) +
+                                       (per_product ? split * p.a_rstride : 0));
+        const int64_t boff = uniform64((p.table ? p.table[2 * z + 1] : z * p.b_bstride) +
+                                       (per_product ? split * p.b_rstride : 0));
         const bool masked = p.relu_mask && p.splits == 1;
         f16v mk[2][2][2];       // fused ReLU mask of a block of C: [block parity][i][j]
         f16v acc[2][QN][2][2];  // [A half][B half][block i][block j]
@@ -1396,7 +1401,9 @@ int big_tiles(int64_t M, int64_t N, int64_t K, int64_t batch, int64_t reduce, in
     const int64_t tiles_half = ((M + BT - 1) / BT) * ((N + 127) / 128) * batch;
     const int64_t tiles128 = ((M + BM - 1) / BM) * ((N + BN - 1) / BN) * batch;
     const int64_t slices = (K + BK - 1) / BK;
-    if (reduce != 1 || (masked && slices < 64)) return 0;
+    if (reduce > 1)  // one product per split, at least half a round of 256 x 128 tiles
+        return tiles_half * reduce <= cu_count && 2 * tiles_half * reduce >= cu_count && slices >= 32 ? 128 : 0;
+    if (masked && slices < 64) return 0;
     if (tiles >= cu_count && slices >= 32) return 256;
     if (tiles_half >= cu_count && slices >= 32) return 128;
     if (tiles128 < 2 * int64_t(cu_count) && 2 * tiles_half >= cu_count && slices >= 64) return 128;
@@ -1478,11 +1485,17 @@ void gemm(const float* a, const float* b, float* c, int64_t M, int64_t N, int64_
     } else {
         vec = vec && a_bstride % 4 == 0 && b_bstride % 4 == 0;
     }
-    const bool big_fits = vec && widest * BT < kMax && reduce == 1 && batch <= 65535 / 32;
-    const int big_n = !big_fits                   ? 0
-                      : mode == kGemmTiles256     ? 256
-                      : mode == kGemmTiles256x128 ? 128
-                      : automatic && !small && !simple
+    // A batch reduction takes the 256-row tiles only when it splits one
+    // product per split (r_per_split 1 below): output tiles times products
+    // within one workgroup per CU.
+    const auto reduce_fits = [&](int64_t width) {
+        return reduce == 1 || ((M + BT - 1) / BT) * ((N + width - 1) / width) * batch * reduce <= d.cu_count;
+    };
+    const bool big_fits = vec && widest * BT < kMax && batch <= 65535 / 32;
+    const int big_n = !big_fits                                        ? 0
+                      : mode == kGemmTiles256                          ? (reduce_fits(256) ? 256 : 0)
+                      : mode == kGemmTiles256x128                      ? (reduce_fits(128) ? 128 : 0)
+                      : automatic && !small && !simple && reduce_fits(128)
                           ? big_tiles(M, N, K, batch, reduce, d.cu_count, relu_mask != nullptr)
                           : 0;
     const bool big = big_n != 0;

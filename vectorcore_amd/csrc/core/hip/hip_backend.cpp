@@ -50,6 +50,11 @@ class HipStorage;
 
 // A forward product recorded but not launched yet:
 // C = A [m, k] @ B [k, n] (+ bias [n] on every row) (then ReLU), all contiguous.
+// Layer products below this many outputs take kernels that write no ReLU
+// bits (the 256-row tiles need a full round of workgroups): no bits buffer
+// is requested for them.
+constexpr std::size_t kReluBitsMinElements = std::size_t(1) << 20;
+
 struct DeferredProduct {
     std::shared_ptr<HipStorage> a, b, bias;
     std::size_t a_offset = 0, b_offset = 0, bias_offset = 0;
@@ -136,7 +141,7 @@ public:
         if (deferred_) {
             const DeferredProduct& d = *deferred_;
             const float* bias = d.bias ? d.bias->ptr() + d.bias_offset : nullptr;
-            if (d.relu) {
+            if (d.relu && d.m * d.n >= kReluBitsMinElements) {
                 // With the layer's ReLU bitmask where its kernel writes one,
                 // for the product that applies the ReLU's backward rule.
                 auto bits = std::make_shared<HipStorage>((d.m + 31) / 32 * d.n);
@@ -152,7 +157,7 @@ public:
                 }
             } else {
                 check(vc_hip_matmul_bias_relu(d.a->ptr() + d.a_offset, d.b->ptr() + d.b_offset,
-                                              static_cast<float*>(ptr_), d.m, d.k, d.n, bias, 0),
+                                              static_cast<float*>(ptr_), d.m, d.k, d.n, bias, d.relu ? 1 : 0),
                       "HIP matmul failed");
             }
             deferred_.reset();  // drops the operands

@@ -214,3 +214,34 @@ def test_train_step_reads_the_relu_masks_as_bits():
     # and 1/8 byte of mask per element
     want = sum(4.0 * (m * kk + kk * n + m * n) + m * n / 8.0 for kk, n in ((100, 4096), (4096, 4096)))
     assert nt["bytes"] == want
+
+
+def test_bits_random_sweep():
+    """Seeded random shapes (tile edges, odd sizes, aligned and not), transposes
+    and kernel settings: the product masked by bits is the float-mask
+    product's bits, and the layer product's bits are [c > 0] where written."""
+    rng = np.random.default_rng(2024)
+    edges = [1, 3, 4, 31, 32, 33, 64, 127, 128, 129, 255, 256, 257, 300, 513]
+    z0 = C.sizes([0])
+    for case in range(40):
+        m, n = (int(rng.choice(edges)) if rng.random() < 0.5 else int(rng.integers(1, 700)) for _ in range(2))
+        k = int(rng.choice([1, 4, 16, 32, 33, 64, 100, 256, 300]))
+        ta, tb = int(rng.random() < 0.3), int(rng.random() < 0.6)
+        kernel = KERNELS[case % len(KERNELS)]
+        a, b, mask = masked_pair(m, k, n, ta, tb, 1000 + case)
+        da, db, dm = C.Buffer.of(a), C.Buffer.of(b), C.Buffer.of(mask)
+        dw = C.Buffer.of(pack_relu_bits(mask), dtype=np.uint32)
+        with C.gemm_kernel(kernel):
+            want, got = C.Buffer((m, n)), C.Buffer((m, n))
+            C.check(C.lib().vc_hip_matmul_relu_mask(da.ptr, db.ptr, want.ptr, m, k, n, z0, z0, 1, ta, tb, dm.ptr))
+            C.check(C.lib().vc_hip_matmul_relu_bits(da.ptr, db.ptr, got.ptr, m, k, n, ta, tb, dw.ptr))
+            np.testing.assert_array_equal(got.numpy(), want.numpy(), err_msg=f"case {case}: {m}x{k}x{n} "
+                                          f"ta={ta} tb={tb} {kernel}")
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            w = rng.standard_normal((k, n)).astype(np.float32)
+            bias = rng.standard_normal(n).astype(np.float32)
+            c, plain, words, written = bias_relu_bits(x, w, bias)
+        np.testing.assert_array_equal(c, plain, err_msg=f"case {case}")
+        if written:
+            keep = valid_bits(m, n)
+            np.testing.assert_array_equal(words & keep, pack_relu_bits(c) & keep, err_msg=f"case {case}")

@@ -250,14 +250,15 @@ __global__ __launch_bounds__(kBlock) void colsum_tile_kernel(const float* __rest
 constexpr int kMaxFinishChunks = 1 << 16;
 __device__ unsigned int g_colsum_done[kMaxFinishChunks];
 
-template <bool Vec>
-__global__ __launch_bounds__(kBlock) void colsum_finish_kernel(const float* __restrict__ x, double* __restrict__ part,
-                                                               float* __restrict__ out, int64_t len, int64_t inner,
-                                                               int64_t seg_len) {
+template <bool Vec, int Block>
+__global__ __launch_bounds__(Block) void colsum_finish_kernel(const float* __restrict__ x, double* __restrict__ part,
+                                                              float* __restrict__ out, int64_t len, int64_t inner,
+                                                              int64_t seg_len) {
     constexpr int W = Vec ? 4 : 1;
-    constexpr int kWaves = kBlock / kWave;
+    constexpr int kWaves = Block / kWave;
+    constexpr int kRows = Block / kColLanes;  // row lanes of a block
     constexpr int kCols = kColLanes * W;      // columns of a block
-    constexpr int kParts = kBlock / kCols;    // threads per column in the final sum
+    constexpr int kParts = Block / kCols;     // threads per column in the final sum
     __shared__ double lds[kWaves][kCols];
     __shared__ int last_block;
     const int c = threadIdx.x % kColLanes, rl = threadIdx.x / kColLanes;
@@ -283,18 +284,18 @@ __global__ __launch_bounds__(kBlock) void colsum_finish_kernel(const float* __re
     for (int w = 0; w < W; ++w) acc[w] = 0.0;
     if (col < inner) {
         const float* base = x + col;
-        for (int64_t a = a0 + rl; a < a1; a += kColInFlight * kRowLanes) {
+        for (int64_t a = a0 + rl; a < a1; a += kColInFlight * kRows) {
             // Up to kColInFlight rows, all loaded before the first add.
             if constexpr (Vec) {
                 f4 v[kColInFlight];
 #pragma unroll
                 for (int u = 0; u < kColInFlight; ++u) {
-                    const int64_t r = a + u * kRowLanes;
+                    const int64_t r = a + u * kRows;
                     v[u] = r < a1 ? ld4(base + r * inner) : f4{0.0f, 0.0f, 0.0f, 0.0f};
                 }
 #pragma unroll
                 for (int u = 0; u < kColInFlight; ++u) {
-                    if (a + u * kRowLanes < a1) {
+                    if (a + u * kRows < a1) {
                         acc[0] += double(v[u].x); acc[1] += double(v[u].y); acc[2] += double(v[u].z); acc[3] += double(v[u].w);
                     }
                 }
@@ -302,12 +303,12 @@ __global__ __launch_bounds__(kBlock) void colsum_finish_kernel(const float* __re
                 float v[kColInFlight];
 #pragma unroll
                 for (int u = 0; u < kColInFlight; ++u) {
-                    const int64_t r = a + u * kRowLanes;
+                    const int64_t r = a + u * kRows;
                     v[u] = r < a1 ? base[r * inner] : 0.0f;
                 }
 #pragma unroll
                 for (int u = 0; u < kColInFlight; ++u)
-                    if (a + u * kRowLanes < a1) acc[0] += double(v[u]);
+                    if (a + u * kRows < a1) acc[0] += double(v[u]);
             }
         }
     }
@@ -505,10 +506,29 @@ ColumnPlan column_plan(const float* in, int64_t outer, int64_t len, int64_t inne
 // 8192 x 1000 took 13.9 us, against 12.1-12.4 us for 128 blocks and for the
 // two-launch path, which 4096 x 1000 takes in 8.9 us against 7.3 us here.
 // Below 8 chunks the two-launch path runs. (8192 x 4096 takes 23.9 us in one
-// launch against 26.1 us in two.)
+// launch against 26.1 us in two.) Narrow sums run 512-thread workgroups, twice
+// the rows in flight per block at the same count of partials and counters:
+// 8192 x 1000 11.5 -> 10.2 us, 4096 x 1000 7.3 -> 7.0 us, 8192 x 512 the
+// same 7.0 us; 1024 threads gave 10.3 us on 8192 x 1000 but 7.8 and 8.0 us on
+// the other two, and 256 blocks of 512 threads 11.1 us (back-to-back calls).
+// Wide sums keep 256 threads: 512 or 1024 at 1024-2048 blocks measured the
+// same or slower (1024 threads at 2048 blocks: 39 us on 8192 x 4096).
+#ifndef VC_COLSUM_NARROW_BLOCK
+#define VC_COLSUM_NARROW_BLOCK 512
+#endif
+#ifndef VC_COLSUM_NARROW_BLOCKS
+#define VC_COLSUM_NARROW_BLOCKS 128
+#endif
+#ifndef VC_COLSUM_WIDE_BLOCK
+#define VC_COLSUM_WIDE_BLOCK 256
+#endif
+#ifndef VC_COLSUM_WIDE_BLOCKS
+#define VC_COLSUM_WIDE_BLOCKS 2048
+#endif
 constexpr int64_t kFinishMinChunks = 8, kFinishWideChunks = 32;
 struct FinishPlan {
     bool vec;
+    int block;  // threads per workgroup: 256, 512 or 1024
     int64_t chunks, segs, seg_len;
 };
 
@@ -517,7 +537,9 @@ FinishPlan finish_plan(const float* in, int64_t len, int64_t inner) {
     f.vec = inner % 4 == 0 && aligned16(in);
     const int64_t width = f.vec ? 4 * kColLanes : kColLanes;
     f.chunks = (inner + width - 1) / width;
-    const int64_t blocks = f.chunks >= kFinishWideChunks ? 2048 : 128;
+    const bool wide = f.chunks >= kFinishWideChunks;
+    f.block = wide ? VC_COLSUM_WIDE_BLOCK : VC_COLSUM_NARROW_BLOCK;
+    const int64_t blocks = wide ? VC_COLSUM_WIDE_BLOCKS : VC_COLSUM_NARROW_BLOCKS;
     int64_t segs = std::max<int64_t>(1, (blocks + f.chunks - 1) / f.chunks);
     segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / 16), int64_t(32)});
     f.seg_len = (len + segs - 1) / segs;
@@ -639,10 +661,16 @@ void reduce_axis(const float* in, float* out, int64_t outer, int64_t len, int64_
         if (f.chunks >= kFinishMinChunks && f.chunks <= kMaxFinishChunks && part_bytes < (int64_t(1) << 31)) {
             double* part = static_cast<double*>(memory.take(size_t(part_bytes)));
             const dim3 grid(unsigned(f.chunks), unsigned(f.segs));
-            if (f.vec)
-                launch(colsum_finish_kernel<true>, grid, dim3(kBlock), 0, d.stream, in, part, out, len, inner, f.seg_len);
-            else
-                launch(colsum_finish_kernel<false>, grid, dim3(kBlock), 0, d.stream, in, part, out, len, inner, f.seg_len);
+#define VC_FINISH(VEC, B) \
+    launch(colsum_finish_kernel<VEC, B>, grid, dim3(B), 0, d.stream, in, part, out, len, inner, f.seg_len)
+            if (f.block == 1024) {
+                if (f.vec) VC_FINISH(true, 1024); else VC_FINISH(false, 1024);
+            } else if (f.block == 512) {
+                if (f.vec) VC_FINISH(true, 512); else VC_FINISH(false, 512);
+            } else {
+                if (f.vec) VC_FINISH(true, 256); else VC_FINISH(false, 256);
+            }
+#undef VC_FINISH
             after_launch(label);
             p.done();
             return;

@@ -477,15 +477,18 @@ def reduce_axis_dev(x, axis, op):
 
 @pytest.mark.parametrize("shape", [(64, 500, 33), (5, 300, 7), (4096, 4096), (8192, 1000), (3, 4, 5), (1, 3_000_001),
                                    (8, 1024 * 1024), (3001, 2051), (70, 8192), (2049, 2048), (1000, 700), (3001, 301),
-                                   (3000, 300), (2000, 512), (2000, 448), (1500, 2044), (2000, 2047), (700, 250)])
+                                   (3000, 300), (2000, 512), (2000, 448), (1500, 2044), (2000, 2047), (700, 250),
+                                   (1024, 4096), (600, 4100)])
 def test_reduce_axis_against_oracle(shape):
     # Column sums of one matrix with at least 8 column chunks (64 columns
     # each with 16-byte loads, 16 with scalar loads) take the one-launch
     # kernel (the last block of each column chunk adds the partials): about
     # 2048 blocks from 32 chunks up, as (4096, 4096) and (2049, 2048) with
     # 16-byte loads, (3001, 2051) with scalar loads and short last segments,
-    # (70, 8192) with 4 segments; about 128 below, as (8192, 1000), (1000, 700)
-    # with a short last chunk and (3001, 301) with scalar loads. (3000, 300)
+    # (1024, 4096) with 4 segments and (600, 4100) with 2 (segments of at
+    # least 256 rows), (70, 8192) with one; about 128 below, as (8192, 1000),
+    # (1000, 700) with a short last chunk and 3 short segments and (3001, 301)
+    # with scalar loads. (3000, 300)
     # has 5 chunks: partials, then a combine launch. At the boundaries:
     # (2000, 512) has 8 chunks (one launch), (2000, 448) 7 (two launches),
     # (1500, 2044) 32 with a short last one (about 2048 blocks). Rows that

@@ -498,7 +498,7 @@ ColumnPlan column_plan(const float* in, int64_t outer, int64_t len, int64_t inne
 }
 
 // The one-launch column sum (outer 1): about 2048 blocks from 32 chunks
-// (2048 columns) up, about 128 from 8 to 31 chunks; segments of at least 16
+// (2048 columns) up, about 128 from 8 to 31 chunks; segments of at least 256
 // rows, at most 32 segments (the blocks of a chunk count in on one counter,
 // and atomics on one address are served one at a time: 128 segments per chunk
 // measured 2.5x slower than 32); a function of the shape only. Narrow sums
@@ -525,6 +525,15 @@ ColumnPlan column_plan(const float* in, int64_t outer, int64_t len, int64_t inne
 #ifndef VC_COLSUM_WIDE_BLOCKS
 #define VC_COLSUM_WIDE_BLOCKS 2048
 #endif
+// Segments shorter than 256 rows cost more in partials and counter atomics
+// than they give in parallel loads: with the floor at 16 rows, 1024 x 4096
+// ran as 32 segments of 32 rows in 14.6 us; at 256 rows, 4 segments take
+// 6.2-6.4 us (512 x 4096 14.5 -> 5.7, 2048 x 2048 10.6 -> 6.5, 256 x 8192
+// 10.0 -> 5.4 us). A floor of 512 rows lost 23% on 1000 x 4096 (two
+// segments), 1024 lost on most shapes. The step's shapes keep their plans.
+#ifndef VC_COLSUM_MIN_SEG_ROWS
+#define VC_COLSUM_MIN_SEG_ROWS 256
+#endif
 constexpr int64_t kFinishMinChunks = 8, kFinishWideChunks = 32;
 struct FinishPlan {
     bool vec;
@@ -541,7 +550,7 @@ FinishPlan finish_plan(const float* in, int64_t len, int64_t inner) {
     f.block = wide ? VC_COLSUM_WIDE_BLOCK : VC_COLSUM_NARROW_BLOCK;
     const int64_t blocks = wide ? VC_COLSUM_WIDE_BLOCKS : VC_COLSUM_NARROW_BLOCKS;
     int64_t segs = std::max<int64_t>(1, (blocks + f.chunks - 1) / f.chunks);
-    segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / 16), int64_t(32)});
+    segs = std::min<int64_t>({segs, std::max<int64_t>(1, len / VC_COLSUM_MIN_SEG_ROWS), int64_t(32)});
     f.seg_len = (len + segs - 1) / segs;
     f.segs = (len + f.seg_len - 1) / f.seg_len;
     return f;
